@@ -1,0 +1,134 @@
+/* jeff_mlora.h: C ABI of the MI355X (gfx950) batched multi-LoRA INT4 linear.
+ *
+ * One fused group of matrices that read the same input x (T tokens, K inputs) and are stacked along the output:
+ *   y[t, :] = bf16( x[t] W^T  +  bf16(x[t] A_j^T) (sB_j)^T  for each matrix j of the group )
+ * with W = bf16((c - z) s) from packed 4-bit codes, and (A_j, sB_j) read from the pool row of token t's adapter.
+ * Every entry point takes raw device pointers, sizes and a HIP stream, allocates nothing, never synchronises, and
+ * returns MLORA_OK or a negative status before launching anything. No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (paths in the reference checkout, runtime/python/src/jeff_runtime/engine/):
+ *   mlora_route        per-token adapter lookup adp[t // row_len]          fast_path.py:167,189; int4_kernels.py:72,113
+ *   mlora_int4_linear  int4_product (base + LoRA shrink + expand)          int4_kernels.py:132-177
+ *   mlora_lora_add     lora_add (in-place LoRA update of y)                fast_path.py:277-289
+ *   mlora_shrink       the LoRA first factor QP = x A^T (_lora_mid_kernel) fast_path.py:159-177
+ *   mlora_dequant      dequantize / bf16(q * s) of the kernel layout       int4.py:203-208,258-262
+ *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
+ */
+#ifndef JEFF_MLORA_H
+#define JEFF_MLORA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLORA_ABI_VERSION 1
+#define MLORA_MAX_MATS 8            /* matrices per fused group (the reference's largest has 4) */
+#define MLORA_MAX_REQUESTS 8192     /* request rows per routed pass */
+#define MLORA_MAX_POOL_ROWS 262144  /* adapter pool rows (row 0 = the base, no update) */
+
+enum {
+  MLORA_OK = 0,
+  MLORA_EINVAL = -1,       /* a null pointer, a bad size or shape */
+  MLORA_EALIGN = -2,       /* a pointer, stride or offset not 16-byte aligned */
+  MLORA_EOVERFLOW = -3,    /* sizes beyond the kernels' index range */
+  MLORA_EWORKSPACE = -4,   /* workspace too small */
+  MLORA_EUNSUPPORTED = -5, /* a shape this build does not run (group, matrices, requests) */
+  MLORA_ELAUNCH = -6       /* the HIP launch itself failed */
+};
+
+/* Route status bits, written by mlora_route to route->status[0] on the device. */
+#define MLORA_ROUTE_BAD_ADAPTER 1   /* an adapter index outside [0, pool_rows): that row was routed to row 0 */
+#define MLORA_ROUTE_BAD_SEQLENS 2   /* cu_seqlens not 0-based, non-decreasing, ending at tokens: identity routing */
+
+/* Kernel-selection flags (0 = automatic). */
+#define MLORA_FORCE_BASE_GEMV 1
+#define MLORA_FORCE_BASE_MFMA 2
+#define MLORA_FORCE_SHRINK_GEMV 4
+#define MLORA_FORCE_SHRINK_MFMA 8
+
+/* INT4 weights in the kernel layout (reference int4.py:215-230, plus zero points and g128):
+ * words  int32 (k/8, columns): word i of column c holds inputs 8i..8i+7, input 8i+j in bits 4j..4j+3 (the code c);
+ * scales bf16 (k/group, columns); zeros uint8 (k/group, columns) with z in [0, 15], or NULL for z = 8 (symmetric);
+ * columns = out rounded up to 64; padding columns hold code 8, zero 8, scale 1. */
+typedef struct {
+  const int32_t* words;
+  const uint16_t* scales;
+  const uint8_t* zeros;
+  int32_t k, columns, out, group;
+} mlora_int4_t;
+
+/* The adapter pool of one fused group. Row a of the pool (pool + a * pool_stride, bf16) holds, for this group:
+ * at off_a the stacked first factors A (rank_cap, k): matrix j in rows [rho_j, rho_j + cap[j]), rho_j = sum of the
+ * caps before j; at off_b[j] the second factor of matrix j, sB_j (cols[j], cap[j]), row n = output n's rank vector.
+ * ranks[a * ranks_stride + j] is the live rank of matrix j in row a (0: no update); only rows [0, rank) of A_j and
+ * columns [0, rank) of sB_j are read. Row 0 is the base and must have all ranks 0. */
+typedef struct {
+  const uint16_t* pool;
+  const int32_t* ranks;
+  int64_t pool_stride;
+  int64_t off_a;
+  int64_t off_b[MLORA_MAX_MATS];
+  int32_t ranks_stride, pool_rows, n_mats, rank_cap;
+  int32_t cap[MLORA_MAX_MATS];
+  int32_t cols[MLORA_MAX_MATS];
+} mlora_lora_t;
+
+/* A routed pass: request rows sorted (stably) by adapter index, so each adapter's tokens form one segment.
+ * Buffers on the device, written by mlora_route and read by the products:
+ *   req_order (requests)        request rows in sorted order
+ *   tok_perm  (tokens)          sorted token position -> original token index
+ *   last_of   (tokens)          per sorted position, the request whose last token is there, else -1
+ *   seg_start (max_segs + 1)    first sorted position of each segment, then the end
+ *   seg_adapter (max_segs)      the pool row of each segment, increasing
+ *   num_segs, status (1 each)   the number of segments; MLORA_ROUTE_* bits
+ * max_segs must be at least min(requests, pool_rows). */
+typedef struct {
+  int32_t* req_order;
+  int32_t* tok_perm;
+  int32_t* last_of;
+  int32_t* seg_start;
+  int32_t* seg_adapter;
+  int32_t* num_segs;
+  int32_t* status;
+  int64_t tokens;
+  int32_t requests, max_segs;
+} mlora_route_t;
+
+int mlora_abi_version(void);
+
+/* Bytes of device workspace a product over `tokens` tokens of a group with `rank_cap` stacked ranks needs. */
+size_t mlora_workspace_bytes(int64_t tokens, int32_t rank_cap);
+
+/* Route a pass: adp int32 (requests) pool rows; either cu_seqlens int32 (requests + 1) token offsets or, when it
+ * is NULL, rows of row_len tokens each (tokens = requests * row_len). One launch. */
+int mlora_route(const int32_t* adp, const int32_t* cu_seqlens, int32_t row_len, const mlora_route_t* route,
+                int32_t pool_rows, void* stream);
+
+/* The dequantised weights bf16((c - z) s) of `w` as bf16 (out, k), row-major. */
+int mlora_dequant(const mlora_int4_t* w, uint16_t* out, void* stream);
+
+/* The LoRA first factor of every routed token: mid (tokens, rank_cap) bf16 at sorted positions, matrix j's live
+ * ranks in columns [rho_j, rho_j + rank); other columns are not written. */
+int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
+                 int32_t k, uint16_t* mid, int32_t flags, void* stream);
+
+/* y (tokens, w->out) bf16 = x W^T + each token's LoRA update, one rounding per output; x (tokens, k) bf16 rows
+ * x_stride elements apart (k a multiple of 64, rows 16-byte aligned). last_out (requests, w->out) bf16 or NULL:
+ * each request's last-token output row as well. */
+int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                      const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                      void* workspace, size_t workspace_bytes, int32_t flags, void* stream);
+
+/* In place: y (tokens, n_out) bf16 += each token's LoRA update (y read in float32, one rounding); x (tokens, k). */
+int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
+                   int32_t k, uint16_t* y, int64_t y_stride, int32_t n_out, void* workspace, size_t workspace_bytes,
+                   int32_t flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JEFF_MLORA_H */

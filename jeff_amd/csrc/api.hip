@@ -1,0 +1,155 @@
+// The C ABI (include/jeff_mlora.h): argument checks, then kernel launches on the caller's stream.
+// Every check runs on the host, before any launch; nothing here allocates, synchronises or reads device memory, so
+// the entry points can be recorded into a HIP graph.
+#include <climits>
+
+#include "mlora_common.h"
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_route(const mlora_route_t* r) {
+  if (r == nullptr || r->tokens < 0 || r->requests < 0 || r->max_segs < 0) return MLORA_EINVAL;
+  if (r->tokens >= INT_MAX) return MLORA_EOVERFLOW;
+  if (r->requests > MLORA_MAX_REQUESTS) return MLORA_EUNSUPPORTED;
+  if (r->num_segs == nullptr || r->seg_start == nullptr || r->seg_adapter == nullptr || r->status == nullptr)
+    return MLORA_EINVAL;
+  if (r->tokens > 0 && (r->tok_perm == nullptr || r->last_of == nullptr)) return MLORA_EINVAL;
+  if (r->requests > 0 && r->req_order == nullptr) return MLORA_EINVAL;
+  return MLORA_OK;
+}
+
+int check_lora(const mlora_lora_t* L, int32_t k, int32_t n_out) {
+  if (L == nullptr || L->pool == nullptr || L->ranks == nullptr) return MLORA_EINVAL;
+  if (k <= 0 || k % 64) return MLORA_EINVAL;  // the kernels stage x in chunks of 64 inputs
+  if (L->n_mats < 1 || L->n_mats > MLORA_MAX_MATS) return MLORA_EUNSUPPORTED;
+  if (L->pool_rows < 1 || L->pool_rows > MLORA_MAX_POOL_ROWS || L->ranks_stride < L->n_mats) return MLORA_EINVAL;
+  if (!aligned16(L->pool) || L->pool_stride % 8 || L->off_a % 8 || L->off_a < 0) return MLORA_EALIGN;
+  int64_t caps = 0, cols = 0;
+  for (int j = 0; j < L->n_mats; ++j) {
+    if (L->cap[j] < 0 || L->cols[j] <= 0) return MLORA_EINVAL;
+    if (L->cap[j] % 8 || L->off_b[j] % 8 || L->off_b[j] < 0) return MLORA_EALIGN;
+    if (L->off_b[j] + (int64_t)L->cols[j] * L->cap[j] > L->pool_stride) return MLORA_EINVAL;
+    caps += L->cap[j];
+    cols += L->cols[j];
+  }
+  if (caps != L->rank_cap || cols != n_out) return MLORA_EINVAL;
+  if (L->off_a + caps * k > L->pool_stride) return MLORA_EINVAL;
+  return MLORA_OK;
+}
+
+int check_int4(const mlora_int4_t* w) {
+  if (w == nullptr || w->words == nullptr || w->scales == nullptr) return MLORA_EINVAL;
+  if (w->group != 64 && w->group != 128) return MLORA_EUNSUPPORTED;
+  if (w->k <= 0 || w->k % w->group || w->columns <= 0 || w->columns % 64 || w->out <= 0 || w->out > w->columns)
+    return MLORA_EINVAL;
+  if (!aligned16(w->words)) return MLORA_EALIGN;
+  if ((int64_t)(w->k / 8) * w->columns >= INT_MAX) return MLORA_EOVERFLOW;
+  return MLORA_OK;
+}
+
+int check_rows(const void* p, int64_t stride, int32_t width) {
+  if (p == nullptr || stride < width) return MLORA_EINVAL;
+  if (!aligned16(p) || stride % 8) return MLORA_EALIGN;
+  return MLORA_OK;
+}
+
+bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
+  if (flags & MLORA_FORCE_SHRINK_MFMA) return true;
+  if (flags & MLORA_FORCE_SHRINK_GEMV) return false;
+  const int64_t segs = r->requests < pool_rows ? r->requests : pool_rows;
+  return r->tokens >= 16 * (segs > 0 ? segs : 1);  // long segments on average: prefill
+}
+
+}  // namespace
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+int mlora_abi_version(void) { return MLORA_ABI_VERSION; }
+
+size_t mlora_workspace_bytes(int64_t tokens, int32_t rank_cap) {
+  if (tokens <= 0 || rank_cap <= 0) return 256;
+  return ((size_t)tokens * (size_t)rank_cap * 2 + 255) & ~(size_t)255;
+}
+
+int mlora_route(const int32_t* adp, const int32_t* cu_seqlens, int32_t row_len, const mlora_route_t* route,
+                int32_t pool_rows, void* stream) {
+  int rc = check_route(route);
+  if (rc) return rc;
+  if (pool_rows < 1 || pool_rows > MLORA_MAX_POOL_ROWS) return MLORA_EINVAL;
+  if (route->requests > 0 && adp == nullptr) return MLORA_EINVAL;
+  const int32_t need = route->requests < pool_rows ? route->requests : pool_rows;
+  if (route->max_segs < need || (route->requests > 0 && route->max_segs < 1)) return MLORA_EINVAL;
+  if (cu_seqlens == nullptr && (row_len < 0 || (int64_t)route->requests * row_len != route->tokens))
+    return MLORA_EINVAL;
+  return launch_route(adp, cu_seqlens, row_len, *route, pool_rows, static_cast<hipStream_t>(stream));
+}
+
+int mlora_dequant(const mlora_int4_t* w, uint16_t* out, void* stream) {
+  int rc = check_int4(w);
+  if (rc) return rc;
+  if (out == nullptr) return MLORA_EINVAL;
+  if (!aligned16(out) || w->k % 8) return MLORA_EALIGN;
+  return launch_dequant(*w, out, static_cast<hipStream_t>(stream));
+}
+
+int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
+                 int32_t k, uint16_t* mid, int32_t flags, void* stream) {
+  int rc = check_route(route);
+  if (rc) return rc;
+  if (lora == nullptr || k <= 0 || k % 64) return MLORA_EINVAL;
+  int32_t n_out = 0;
+  for (int j = 0; j < lora->n_mats && j < MLORA_MAX_MATS; ++j) n_out += lora->cols[j];
+  if ((rc = check_lora(lora, k, n_out))) return rc;
+  if (route->tokens == 0) return MLORA_OK;
+  if ((rc = check_rows(x, x_stride, k))) return rc;
+  if (mid == nullptr) return MLORA_EINVAL;
+  return launch_shrink(*lora, *route, x, x_stride, k, mid, shrink_on_mfma(route, lora->pool_rows, flags),
+                       static_cast<hipStream_t>(stream));
+}
+
+int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                      const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                      void* workspace, size_t workspace_bytes, int32_t flags, void* stream) {
+  int rc = check_int4(w);
+  if (rc) return rc;
+  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
+  if (route->tokens == 0) return MLORA_OK;
+  if ((rc = check_rows(x, x_stride, w->k))) return rc;
+  if (y == nullptr || y_stride < w->out) return MLORA_EINVAL;
+  if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
+  if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
+  const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
+  if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* mid = static_cast<uint16_t*>(workspace);
+  if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, shrink_on_mfma(route, lora->pool_rows, flags), s)))
+    return rc;
+  return launch_base(w, *lora, *route, x, x_stride, y, y_stride, last_out, w->out, mid, gemv, s);
+}
+
+int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
+                   int32_t k, uint16_t* y, int64_t y_stride, int32_t n_out, void* workspace, size_t workspace_bytes,
+                   int32_t flags, void* stream) {
+  int rc = check_route(route);
+  if (rc) return rc;
+  if (k <= 0 || k % 64 || n_out <= 0) return MLORA_EINVAL;
+  if ((rc = check_lora(lora, k, n_out))) return rc;
+  if (route->tokens == 0) return MLORA_OK;
+  if ((rc = check_rows(x, x_stride, k))) return rc;
+  if (y == nullptr || y_stride < n_out) return MLORA_EINVAL;
+  if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
+  if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
+  const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
+  if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* mid = static_cast<uint16_t*>(workspace);
+  if ((rc = launch_shrink(*lora, *route, x, x_stride, k, mid, shrink_on_mfma(route, lora->pool_rows, flags), s)))
+    return rc;
+  return launch_base(nullptr, *lora, *route, x, x_stride, y, y_stride, nullptr, n_out, mid, gemv, s);
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

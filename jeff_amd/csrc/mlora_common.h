@@ -1,0 +1,134 @@
+// Device helpers shared by the gfx950 kernels of the multi-LoRA INT4 linear.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "jeff_mlora.h"
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace mlora {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
+// Two float32 values rounded to nearest even and packed as bf16 (lo in bits 0..15): one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+// The 8 weights of one packed word (input j of the 8 in bits 4j..4j+3) as bf16((c - z) s), in input order.
+// fma(c, s, -z s) is exact for every finite scale below 2^120: c s and z s are products of a 4-bit integer and an
+// 8-bit significand, and their difference has at most 13 significant bits, so the single rounding to bf16 is the
+// only one. zs = z * s is formed once per (group, column) by the caller.
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float zs) {
+  uint32_t lo = w & 0x0F0F0F0Fu;         // codes of inputs 0, 2, 4, 6 in bytes 0..3
+  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // codes of inputs 1, 3, 5, 7
+  // keep the byte layout visible to the compiler so each code converts with one v_cvt_f32_ubyteN
+  asm volatile("" : "+v"(lo));
+  asm volatile("" : "+v"(hi));
+  const float c0 = (float)(lo & 0xFF), c2 = (float)((lo >> 8) & 0xFF);
+  const float c4 = (float)((lo >> 16) & 0xFF), c6 = (float)(lo >> 24);
+  const float c1 = (float)(hi & 0xFF), c3 = (float)((hi >> 8) & 0xFF);
+  const float c5 = (float)((hi >> 16) & 0xFF), c7 = (float)(hi >> 24);
+  uint4 r;
+  r.x = pack_bf16x2(__builtin_fmaf(c0, s, -zs), __builtin_fmaf(c1, s, -zs));
+  r.y = pack_bf16x2(__builtin_fmaf(c2, s, -zs), __builtin_fmaf(c3, s, -zs));
+  r.z = pack_bf16x2(__builtin_fmaf(c4, s, -zs), __builtin_fmaf(c5, s, -zs));
+  r.w = pack_bf16x2(__builtin_fmaf(c6, s, -zs), __builtin_fmaf(c7, s, -zs));
+  return r;
+}
+
+// Keep the first n of 8 packed bf16 values, zero the rest (n <= 0: all zero, n >= 8: unchanged).
+__device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
+  if (n >= 8) return v;
+  uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo = 2 * i, hi = 2 * i + 1;
+    uint32_t m = (lo < n ? 0x0000FFFFu : 0u) | (hi < n ? 0xFFFF0000u : 0u);
+    e[i] &= m;
+  }
+  return make_uint4(e[0], e[1], e[2], e[3]);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 8 products of bf16 pairs accumulated into acc with v_dot2_f32_bf16, in pair order.
+__device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x), __builtin_bit_cast(bf16x2_t, b.x), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y), __builtin_bit_cast(bf16x2_t, b.y), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z), __builtin_bit_cast(bf16x2_t, b.z), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w), __builtin_bit_cast(bf16x2_t, b.w), acc,
+                                        false);
+  return acc;
+}
+
+// The segment s with seg_start[s] <= p < seg_start[s + 1], for 0 <= p < seg_start[nseg] (binary search).
+__device__ __forceinline__ int segment_of(const int32_t* seg_start, int nseg, int64_t p) {
+  int lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seg_start[mid] <= p) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Live rank of matrix j in pool row a, clamped to [0, cap] so a corrupt table cannot move a read out of the row.
+__device__ __forceinline__ int live_rank(const mlora_lora_t& L, int a, int j) {
+  int r = L.ranks[(int64_t)a * L.ranks_stride + j];
+  r = r < 0 ? 0 : r;
+  return r > L.cap[j] ? L.cap[j] : r;
+}
+
+// Stacked-rank offset rho_j and output-column offset of matrix j.
+__device__ __forceinline__ int rank_offset(const mlora_lora_t& L, int j) {
+  int o = 0;
+  for (int i = 0; i < j; ++i) o += L.cap[i];
+  return o;
+}
+__device__ __forceinline__ int col_offset(const mlora_lora_t& L, int j) {
+  int o = 0;
+  for (int i = 0; i < j; ++i) o += L.cols[i];
+  return o;
+}
+// The matrix whose output columns hold column c (c < sum of cols).
+__device__ __forceinline__ int matrix_of(const mlora_lora_t& L, int c) {
+  int j = 0, o = L.cols[0];
+  while (j + 1 < L.n_mats && c >= o) {
+    ++j;
+    o += L.cols[j];
+  }
+  return j;
+}
+
+}  // namespace mlora
+
+// Launchers (one per kernel family), defined in their .hip files; each returns MLORA_OK or MLORA_ELAUNCH.
+int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const mlora_route_t& r, int32_t pool_rows,
+                 hipStream_t stream);
+int launch_dequant(const mlora_int4_t& w, uint16_t* out, hipStream_t stream);
+int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x, int64_t x_stride, int32_t k,
+                  uint16_t* mid, bool mfma, hipStream_t stream);
+int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
+                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+                const uint16_t* mid, bool gemv, hipStream_t stream);

@@ -1,0 +1,192 @@
+// Adapter routing: request rows -> segments of the sorted order, one segment per adapter present.
+// Replaces the reference's per-tile lookup adp[t // row_len] (engine/fast_path.py:167,189;
+// engine/int4_kernels.py:72,113) with a stable sort, so every adapter's tokens are contiguous.
+#include "mlora_common.h"
+
+namespace {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kIndexBits = 13;  // request index in the low bits of a sort key: MLORA_MAX_REQUESTS = 2^13
+static_assert((1 << kIndexBits) == MLORA_MAX_REQUESTS, "key layout");
+static_assert(MLORA_MAX_POOL_ROWS <= (1 << (31 - kIndexBits)), "a key must stay below the padding key");
+
+// Exclusive prefix sum of one value per thread over the 1024-thread block (16 waves), in thread order.
+__device__ int block_exclusive_scan(int v, int* wave_sums, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_sums[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < 16 ? wave_sums[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(w, o);
+      if (lane >= o) w += y;
+    }
+    if (lane < 16) wave_sums[lane] = w;
+  }
+  __syncthreads();
+  const int before = wave == 0 ? 0 : wave_sums[wave - 1];
+  *total = wave_sums[15];
+  __syncthreads();
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __restrict__ adp,
+                                                             const int32_t* __restrict__ cu, int32_t row_len,
+                                                             mlora_route_t r, int32_t pool_rows) {
+  __shared__ uint32_t keys[MLORA_MAX_REQUESTS];
+  __shared__ int32_t pstart[MLORA_MAX_REQUESTS];
+  __shared__ int32_t wave_sums[16];
+  __shared__ int32_t status, seq_ok;
+  const int tid = threadIdx.x;
+  const int B = r.requests;
+  const int64_t T = r.tokens;
+  if (tid == 0) {
+    status = 0;
+    seq_ok = 1;
+  }
+  __syncthreads();
+  if (cu != nullptr) {  // the offsets must start at 0, never decrease and end at the token count
+    bool bad = tid == 0 && (cu[0] != 0 || (int64_t)cu[B] != T);
+    for (int i = tid; i < B; i += kRouteThreads) bad |= cu[i + 1] < cu[i];
+    if (bad) atomicAnd(&seq_ok, 0);
+  }
+  __syncthreads();
+  if (!seq_ok) {  // unusable offsets: identity routing through row 0 (no LoRA), flagged
+    for (int64_t p = tid; p < T; p += kRouteThreads) {
+      r.tok_perm[p] = (int32_t)p;
+      r.last_of[p] = -1;
+    }
+    for (int i = tid; i < B; i += kRouteThreads) r.req_order[i] = i;
+    if (tid == 0) {
+      *r.num_segs = 1;
+      r.seg_start[0] = 0;
+      r.seg_start[1] = (int32_t)T;
+      r.seg_adapter[0] = 0;
+      *r.status = MLORA_ROUTE_BAD_SEQLENS;
+    }
+    return;
+  }
+  int n = 1;
+  while (n < B) n <<= 1;
+  bool bad_adapter = false;
+  for (int i = tid; i < n; i += kRouteThreads) {
+    uint32_t key = 0xFFFFFFFFu;  // padding sorts last
+    if (i < B) {
+      int a = adp[i];
+      if (a < 0 || a >= pool_rows) {
+        a = 0;
+        bad_adapter = true;
+      }
+      key = ((uint32_t)a << kIndexBits) | (uint32_t)i;  // unique keys: any sort of them is stable
+    }
+    keys[i] = key;
+  }
+  if (bad_adapter) atomicOr(&status, MLORA_ROUTE_BAD_ADAPTER);
+  __syncthreads();
+  for (int k = 2; k <= n; k <<= 1) {  // bitonic sort, ascending
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < n; i += kRouteThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint32_t a = keys[i], b = keys[ixj];
+          const bool up = (i & k) == 0;
+          if ((a > b) == up) {
+            keys[i] = b;
+            keys[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // lengths and segment starts of 8 consecutive sorted rows per thread
+  constexpr int kPer = MLORA_MAX_REQUESTS / kRouteThreads;
+  int len[kPer], ada[kPer], rho[kPer];
+  bool first[kPer];
+  int lsum = 0, fsum = 0;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = tid * kPer + e;
+    len[e] = 0;
+    first[e] = false;
+    ada[e] = 0;
+    rho[e] = 0;
+    if (i < B) {
+      const uint32_t key = keys[i];
+      rho[e] = (int)(key & ((1u << kIndexBits) - 1));
+      ada[e] = (int)(key >> kIndexBits);
+      len[e] = cu != nullptr ? cu[rho[e] + 1] - cu[rho[e]] : row_len;
+      first[e] = i == 0 || (keys[i - 1] >> kIndexBits) != (uint32_t)ada[e];
+    }
+    lsum += len[e];
+    fsum += first[e] ? 1 : 0;
+  }
+  int ltot, ftot;
+  int run = block_exclusive_scan(lsum, wave_sums, &ltot);
+  int seg = block_exclusive_scan(fsum, wave_sums, &ftot);
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = tid * kPer + e;
+    if (i < B) {
+      pstart[i] = run;
+      r.req_order[i] = rho[e];
+      if (first[e]) {
+        r.seg_adapter[seg] = ada[e];
+        r.seg_start[seg] = run;
+        ++seg;
+      }
+      run += len[e];
+    }
+  }
+  if (tid == 0) {
+    *r.num_segs = ftot;
+    r.seg_start[ftot] = ltot;
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int i = wave; i < B; i += kRouteThreads / 64) {  // one request per wave, its tokens across the lanes
+    const int q = (int)(keys[i] & ((1u << kIndexBits) - 1));
+    const int start = cu != nullptr ? cu[q] : q * row_len;
+    const int l = cu != nullptr ? cu[q + 1] - cu[q] : row_len;
+    const int ps = pstart[i];
+    for (int t = lane; t < l; t += 64) {
+      r.tok_perm[ps + t] = start + t;
+      r.last_of[ps + t] = t == l - 1 ? q : -1;
+    }
+  }
+  if (tid == 0) *r.status = status;
+}
+
+__global__ __launch_bounds__(256) void dequant_kernel(mlora_int4_t w, uint16_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int words_per_col = w.k / 8;
+  if (idx >= (int64_t)words_per_col * w.out) return;
+  const int c = (int)(idx / words_per_col), i = (int)(idx % words_per_col);
+  const int g = (8 * i) / w.group;
+  const float s = mlora::bf16_to_f32(w.scales[(int64_t)g * w.columns + c]);
+  const float z = w.zeros != nullptr ? (float)w.zeros[(int64_t)g * w.columns + c] : 8.0f;
+  const uint32_t word = (uint32_t)w.words[(int64_t)i * w.columns + c];
+  *reinterpret_cast<uint4*>(out + (int64_t)c * w.k + 8 * i) = mlora::dequant_word(word, s, z * s);
+}
+
+}  // namespace
+
+int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const mlora_route_t& r, int32_t pool_rows,
+                 hipStream_t stream) {
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
+  return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
+}
+
+int launch_dequant(const mlora_int4_t& w, uint16_t* out, hipStream_t stream) {
+  const int64_t n = (int64_t)(w.k / 8) * w.out;
+  if (n == 0) return MLORA_OK;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, out);
+  return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
+}

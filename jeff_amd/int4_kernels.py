@@ -1,0 +1,61 @@
+"""int4_product: a fused group's INT4 base product plus each token's LoRA update, on the HIP library.
+
+Mirrors the reference's engine/int4_kernels.py:132-177 (int4_product(lin, x, ws, adp, tiles=None)): same arguments,
+a new bf16 (tokens, lin.out) result, ValueError before any allocation or launch for a group without INT4 weights, an
+input that is not a contiguous bf16 (tokens, lin.k) tensor, or a pass too large for the kernels. Two launches on
+the current stream (the LoRA first factor, then the base product with the second factor fused into its epilogue,
+rounded once), plus the routing launch when the workspace has not routed `adp` yet. Deterministic: no atomic
+additions, every sum in a fixed order."""
+
+from __future__ import annotations
+
+import torch
+
+from jeff_amd import _lib
+from jeff_amd.fast_path import DT, Lin, Workspace, _check_input
+from jeff_amd.int4_tiles import Int4Tiles
+
+
+def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, tiles: Int4Tiles | None = None,
+                 last_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The fused product of x (M, in) through `lin`'s INT4 weights plus each token's adapter update (the pool row of
+    its request row in adp, or the route ws.route made). `tiles` forces the kernel families (tests); `last_out`
+    (requests, lin.out) bf16 also receives each request's last-token output row."""
+    packed = lin.int4
+    if packed is None:
+        raise ValueError(f"{', '.join(lin.names)}: no INT4 weights (attach_int4 gives them to an INT4 base's fused "
+                         "groups only)")
+    _check_input(lin, x, "the INT4 product")
+    m = x.shape[0]
+    if m >= 2 ** 31 - 1:
+        raise ValueError(f"{', '.join(lin.names)}: {m} tokens reach 2^31; the kernels' token offsets are 32-bit")
+    if tiles is not None and tiles.base == "gemv" and m > 8:
+        raise ValueError(f"the GEMV base product runs at most 8 tokens; got {m}")
+    if lin.rank > ws.max_rank:
+        raise ValueError(f"{', '.join(lin.names)}: stacked rank {lin.rank} exceeds the workspace's {ws.max_rank}")
+    if last_out is not None and (last_out.dtype != DT or last_out.dim() != 2 or last_out.shape[1] != lin.out
+                                 or not last_out.is_contiguous() or last_out.shape[0] < adp.numel()):
+        raise ValueError(f"last_out must be a contiguous bfloat16 (requests, {lin.out}) tensor")
+    r = ws.routed(adp, lin.pool.shape[0], m)
+    y = torch.empty(m, lin.out, device=x.device, dtype=DT)
+    h = _lib.lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(h.mlora_int4_linear(packed.abi(), lin.lora_abi(), r, x.data_ptr(), x.stride(0), y.data_ptr(),
+                                   y.stride(0), 0 if last_out is None else last_out.data_ptr(), ws.mid.data_ptr(),
+                                   ws.mid.numel() * 2, 0 if tiles is None else tiles.flags(), stream),
+               "mlora_int4_linear")
+    return y
+
+
+def shrink(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, mfma: bool | None = None) -> torch.Tensor:
+    """The LoRA first factors the products use, at sorted token positions: a (tokens, lin.rank) bf16 view of the
+    workspace, matrix j's live ranks in columns [rho_j, rho_j + rank) (other columns are left as they were)."""
+    _check_input(lin, x, "shrink")
+    m = x.shape[0]
+    r = ws.routed(adp, lin.pool.shape[0], m)
+    flags = 0 if mfma is None else (_lib.FORCE_SHRINK_MFMA if mfma else _lib.FORCE_SHRINK_GEMV)
+    h = _lib.lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(h.mlora_shrink(lin.lora_abi(), r, x.data_ptr(), x.stride(0), lin.k, ws.mid.data_ptr(), flags, stream),
+               "mlora_shrink")
+    return ws.mid[:m * lin.rank].view(m, lin.rank)

@@ -1,0 +1,44 @@
+"""Which HIP kernels run an INT4 product of a given shape (kept apart from the library so the rule can be checked
+without a GPU). The reference chooses Triton tiles here (engine/int4_tiles.py:57-71); the MI355X kernels pick a
+kernel family instead, and the tiles inside each family are fixed for gfx950.
+
+- base: "gemv" (at most GEMV_MAX_TOKENS tokens: one pass over the weights, every token dotted with each dequantised
+  word) or "mfma" (32x32x16 bf16 MFMA tiles of 128 tokens x 128 columns).
+- shrink (the LoRA first factor): "gemv" when segments are short on average (decode: one workgroup streams 16 ranks
+  of one adapter's A) or "mfma" when they are long (prefill: 64-token tiles on MFMA).
+The library makes the same choice itself when no flag forces one (api.hip, shrink_on_mfma)."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from jeff_amd import _lib
+
+GEMV_MAX_TOKENS = 8
+SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT = 16
+BASES = ("gemv", "mfma")
+SHRINKS = ("gemv", "mfma")
+
+
+@dataclass(frozen=True)
+class Int4Tiles:
+    base: str
+    shrink: str
+
+    def flags(self) -> int:
+        f = _lib.FORCE_BASE_GEMV if self.base == "gemv" else _lib.FORCE_BASE_MFMA
+        return f | (_lib.FORCE_SHRINK_GEMV if self.shrink == "gemv" else _lib.FORCE_SHRINK_MFMA)
+
+
+def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = None,
+               pool_rows: int | None = None) -> Int4Tiles:
+    """The kernels for `tokens` tokens in `requests` request rows through a group of `inputs` inputs and `columns`
+    kernel columns; ValueError for a shape the kernels cannot run."""
+    if columns <= 0 or columns % 64 or inputs <= 0 or inputs % 64 or tokens <= 0:
+        raise ValueError(f"The INT4 kernels need columns and inputs that are positive multiples of 64 and at least one "
+                         f"token; got {columns} columns, {inputs} inputs, {tokens} tokens")
+    base = "gemv" if tokens <= GEMV_MAX_TOKENS else "mfma"
+    requests = tokens if requests is None else requests
+    segs = max(1, min(requests, pool_rows if pool_rows is not None else requests))
+    shrink = "mfma" if tokens >= SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT * segs else "gemv"
+    return Int4Tiles(base, shrink)

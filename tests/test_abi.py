@@ -1,0 +1,65 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/jeff_mlora.h declares (and nothing
+else), its constants match the header, and its host-only calls answer (no kernel runs here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+from jeff_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "jeff_mlora.h"
+
+
+def declared() -> set[str]:
+    return set(re.findall(r"^\w[\w\s\*]*?\b(mlora_\w+)\(", HEADER.read_text(), flags=re.M))
+
+
+def test_every_declared_entry_point_is_exported() -> None:
+    names = declared()
+    assert names == set(_lib.EXPORTS)
+    h = _lib.lib()
+    for name in names:
+        assert isinstance(getattr(h, name), ctypes._CFuncPtr)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY)], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {n for n in exported if "mlora" in n} == names  # internal launchers stay hidden
+
+
+def test_header_constants_match_the_binding() -> None:
+    text = HEADER.read_text()
+
+    def const(name: str) -> int:
+        return int(re.search(rf"#define {name} (\d+)", text).group(1))
+
+    assert const("MLORA_ABI_VERSION") == _lib.ABI_VERSION == _lib.lib().mlora_abi_version()
+    assert const("MLORA_MAX_MATS") == _lib.MAX_MATS
+    assert const("MLORA_MAX_REQUESTS") == _lib.MAX_REQUESTS
+    assert const("MLORA_MAX_POOL_ROWS") == _lib.MAX_POOL_ROWS
+    assert const("MLORA_ROUTE_BAD_ADAPTER") == _lib.ROUTE_BAD_ADAPTER
+    assert const("MLORA_ROUTE_BAD_SEQLENS") == _lib.ROUTE_BAD_SEQLENS
+    for name, value in (("MLORA_FORCE_BASE_GEMV", _lib.FORCE_BASE_GEMV), ("MLORA_FORCE_BASE_MFMA", _lib.FORCE_BASE_MFMA),
+                        ("MLORA_FORCE_SHRINK_GEMV", _lib.FORCE_SHRINK_GEMV),
+                        ("MLORA_FORCE_SHRINK_MFMA", _lib.FORCE_SHRINK_MFMA)):
+        assert const(name) == value
+    assert ctypes.sizeof(_lib.Int4) == 8 * 3 + 4 * 4
+    assert ctypes.sizeof(_lib.Lora) == 8 * 4 + 8 * 8 + 4 * 4 + 4 * 16
+
+
+def test_workspace_bytes_and_refusals_before_any_launch() -> None:
+    h = _lib.lib()
+    assert h.mlora_workspace_bytes(100, 48) == 9728 and h.mlora_workspace_bytes(0, 16) == 256
+    # null descriptors and unsupported shapes are refused on the host: nothing reaches a GPU
+    assert h.mlora_dequant(None, None, None) == _lib.EINVAL
+    w = _lib.Int4(16, 16, None, 1024, 3072, 3072, 96)
+    assert h.mlora_dequant(ctypes.byref(w), 16, None) == _lib.EUNSUPPORTED
+    w = _lib.Int4(16, 16, None, 1000, 3072, 3072, 64)
+    assert h.mlora_dequant(ctypes.byref(w), 16, None) == _lib.EINVAL
+    r = _lib.Route(0, 0, 0, 0, 0, 0, 0, 10, _lib.MAX_REQUESTS + 1, 1)
+    assert h.mlora_route(16, None, 1, ctypes.byref(r), 4, None) == _lib.EUNSUPPORTED
+    r = _lib.Route(16, 16, 16, 16, 16, 16, 16, 10, 10, 1)
+    assert h.mlora_route(16, None, 1, ctypes.byref(r), 4, None) == _lib.EINVAL  # max_segs < min(requests, rows)
+    assert h.mlora_route(16, None, 2, ctypes.byref(_lib.Route(16, 16, 16, 16, 16, 16, 16, 10, 10, 4)), 4,
+                         None) == _lib.EINVAL  # 10 rows of 2 tokens are not 10 tokens

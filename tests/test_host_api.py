@@ -1,0 +1,127 @@
+"""The host-side mirror of the reference's interface, checked without a GPU: the pool layout Lin.pack writes, the
+pool's row management, the refusals int4_product makes before any allocation or launch, the kernel choice rule and
+the product registry (the reference's tests/test_product_choice.py expectations)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from jeff_amd.fast_path import DT, AdapterPool, Lin, Workspace, fold_scale
+from jeff_amd.int4 import Int4Error, pack_kernel, pack_kernel_asym, unpack_kernel, unpack_kernel_asym
+from jeff_amd.int4_kernels import int4_product
+from jeff_amd.int4_tiles import Int4Tiles, int4_tiles
+from jeff_amd.product_choice import (CUBLAS, INT4, PAIRS, PRODUCTS, ProductChoice, choose_product,
+                                     product_candidates)
+
+
+def test_pack_writes_a_rows_and_per_matrix_second_factors() -> None:
+    lin = Lin(["l.q_proj", "l.k_proj"], sizes=[24, 16], k=32, ranks=[16, 8])
+    assert lin.rank == 24 and lin.numel() == 24 * 32 + 24 * 16 + 16 * 8
+    pool = AdapterPool([lin], 2, device="cpu")
+    a0, b0 = torch.randn(8, 32).to(DT), torch.randn(24, 8).to(DT)
+    a1, b1 = torch.randn(8, 32).to(DT), torch.randn(16, 8).to(DT)
+    row = pool.add_adapter("x", {"l.q_proj": (a0, b0), "l.k_proj": (a1, b1)})
+    assert row == 1 and pool.ranks[1, :2].tolist() == [8, 8]
+    flat = pool.lora_pool[1]
+    a = flat[:24 * 32].view(24, 32)
+    assert torch.equal(a[0:8], a0) and bool((a[8:16] == 0).all()) and torch.equal(a[16:24], a1)
+    bq = flat[lin.off_bj[0]:lin.off_bj[0] + 24 * 16].view(24, 16)
+    bk = flat[lin.off_bj[1]:lin.off_bj[1] + 16 * 8].view(16, 8)
+    assert torch.equal(bq[:, :8], b0) and bool((bq[:, 8:] == 0).all()) and torch.equal(bk, b1)
+    with pytest.raises(ValueError, match="does not fit the fast path's rank-8 buffer"):
+        pool.add_adapter("big", {"l.k_proj": (torch.zeros(16, 32, dtype=DT), torch.zeros(16, 16, dtype=DT))})
+
+
+def test_pool_rows_lowest_free_first_base_row_zero_and_refusals() -> None:
+    lin = Lin(["l.o_proj"], sizes=[16], k=16)
+    pool = AdapterPool([lin], 3, device="cpu")
+    up = {"l.o_proj": (torch.ones(4, 16, dtype=DT), torch.ones(16, 4, dtype=DT))}
+    assert [pool.add_adapter(n, up) for n in "abc"] == [1, 2, 3]
+    assert pool.index(None) == 0 and bool((pool.lora_pool[0] == 0).all()) and int(pool.ranks[0].abs().sum()) == 0
+    with pytest.raises(ValueError, match="at most 3 adapters"):
+        pool.add_adapter("d", up)
+    with pytest.raises(ValueError, match="already"):
+        pool.add_adapter("a", up)
+    pool.remove_adapter("b", poison=True)
+    assert int(pool.ranks[2].abs().sum()) == 0 and bool(torch.isnan(pool.lora_pool[2].float()).all())
+    assert pool.add_adapter("d", up) == 2 and bool(torch.isfinite(pool.lora_pool[2].float()).all())
+    with pytest.raises(ValueError, match="not loaded"):
+        pool.index("b")
+    pool.remove_adapter("a")
+    with pytest.raises(ValueError, match="does not support"):
+        pool.add_adapter("e", {"l.mlp.gate_proj": up["l.o_proj"]})
+
+
+def test_scale_is_folded_in_float32_then_cast() -> None:
+    b = torch.tensor([[1.0 + 2 ** -7]], dtype=DT)
+    assert float(fold_scale(b, 3.0)) == float(torch.tensor((1.0 + 2 ** -7) * 3.0).to(DT))
+
+
+def test_int4_product_refusals_before_any_launch() -> None:
+    plain = Lin(["layers.0.mlp.down_proj"], [torch.zeros(64, 128, dtype=DT)])
+    ws = Workspace(32, 32, {(128, 64)}, device="cpu")
+    adp = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="no INT4 weights"):
+        int4_product(plain, torch.zeros(32, 128, dtype=DT), ws, adp)
+    plain.int4 = pack_kernel(torch.zeros(64, 128, dtype=torch.int8), torch.ones(64, 2, dtype=DT))
+    with pytest.raises(ValueError, match="bfloat16"):
+        int4_product(plain, torch.zeros(32, 128), ws, adp)
+    with pytest.raises(ValueError, match="contiguous rows"):
+        int4_product(plain, torch.zeros(128, 32, dtype=DT).T, ws, adp)
+    with pytest.raises(ValueError, match="cannot hold whole rows"):
+        Workspace(30, 32)
+
+
+def test_kernel_layout_round_trips_and_refuses() -> None:
+    q = torch.randint(-8, 8, (70, 256), dtype=torch.int8)
+    s = (torch.rand(70, 2) + 0.01).to(DT)
+    p = pack_kernel(q, s, 128)
+    assert tuple(p.words.shape) == (32, 128) and tuple(p.scales.shape) == (2, 128) and p.k == 256
+    back_q, back_s = unpack_kernel(p)
+    assert torch.equal(back_q, q) and torch.equal(back_s, s)
+    codes = torch.randint(0, 16, (70, 256), dtype=torch.uint8)
+    z = torch.randint(0, 16, (70, 2), dtype=torch.uint8)
+    pa = pack_kernel_asym(codes, s, z, 128)
+    c2, s2, z2 = unpack_kernel_asym(pa)
+    assert torch.equal(c2, codes) and torch.equal(s2, s) and torch.equal(z2, z)
+    assert bool((pa.zeros[:, 70:] == 8).all())
+    with pytest.raises(Int4Error, match="finite, positive"):
+        pack_kernel(q, torch.full((70, 2), 2.0 ** 121).to(DT), 128)
+    with pytest.raises(Int4Error, match=r"\[-8, 7\]"):
+        pack_kernel(q.to(torch.int16) + 8, s, 128)
+    with pytest.raises(Int4Error):
+        pack_kernel(q, s, 96)
+
+
+def test_kernel_choice_rule() -> None:
+    assert int4_tiles(4096, 2048, 1) == Int4Tiles("gemv", "gemv")
+    assert int4_tiles(4096, 2048, 8) == Int4Tiles("gemv", "gemv")
+    assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("mfma", "gemv")
+    assert int4_tiles(3072, 1024, 8704, 64, 17) == Int4Tiles("mfma", "mfma")
+    with pytest.raises(ValueError):
+        int4_tiles(100, 1024, 4)
+
+
+GROUPS = ("layers.0.mlp.gate_proj, layers.0.mlp.up_proj", "layers.0.mlp.down_proj")
+
+
+def test_product_registry_follows_the_reference_rules() -> None:
+    assert product_candidates(dict.fromkeys(GROUPS, False)) == (CUBLAS,)
+    assert product_candidates(dict.fromkeys(GROUPS, True)) == PRODUCTS == (CUBLAS, INT4) and PAIRS == 3
+    times = {CUBLAS: [2.4, 9.0, 2.3], INT4: [1.7, 1.6, 8.0]}
+    calls = []
+
+    def timer(kernel: str) -> float:
+        calls.append(kernel)
+        return times[kernel].pop(0)
+
+    assert choose_product(PRODUCTS, timer) == ProductChoice(INT4, {CUBLAS: 2.4, INT4: 1.7})
+    assert calls == [CUBLAS, INT4] * PAIRS
+    assert choose_product(PRODUCTS, lambda k: 1.0) == ProductChoice(CUBLAS, {CUBLAS: 1.0, INT4: 1.0})
+    with pytest.raises(ValueError, match="Unknown product kernel"):
+        product_candidates(dict.fromkeys(GROUPS, True), ["hip"])
+    with pytest.raises(ValueError, match="need an INT4 base"):
+        product_candidates(dict.fromkeys(GROUPS, False), [INT4])
+    with pytest.raises(ValueError, match="hold no INT4 weights"):
+        product_candidates({GROUPS[0]: True, GROUPS[1]: False})
