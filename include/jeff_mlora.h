@@ -11,6 +11,7 @@
  *   mlora_int4_linear  int4_product (base + LoRA shrink + expand)          int4_kernels.py:132-177
  *   mlora_lora_add     lora_add (in-place LoRA update of y)                fast_path.py:277-289
  *   mlora_shrink       the LoRA first factor QP = x A^T (_lora_mid_kernel) fast_path.py:159-177
+ *   mlora_int4_base_expand  the base tiles + LoRA output epilogue          int4_kernels.py:44-64,105-129
  *   mlora_dequant      dequantize / bf16(q * s) of the kernel layout       int4.py:203-208,258-262
  *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
  */
@@ -121,6 +122,12 @@ int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uin
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                       const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
                       void* workspace, size_t workspace_bytes, int32_t flags, void* stream);
+
+/* mlora_int4_linear without its shrink launch: the base product with the LoRA second factor fused into its
+ * epilogue, reading the first factors mid (tokens, rank_cap) that mlora_shrink wrote for the same route and x. */
+int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                           const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                           const uint16_t* mid, int32_t flags, void* stream);
 
 /* In place: y (tokens, n_out) bf16 += each token's LoRA update (y read in float32, one rounding); x (tokens, k). */
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,

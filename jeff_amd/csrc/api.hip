@@ -130,6 +130,21 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
   return launch_base(w, *lora, *route, x, x_stride, y, y_stride, last_out, w->out, mid, gemv, s);
 }
 
+int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                           const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                           const uint16_t* mid, int32_t flags, void* stream) {
+  int rc = check_int4(w);
+  if (rc) return rc;
+  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
+  if (route->tokens == 0) return MLORA_OK;
+  if ((rc = check_rows(x, x_stride, w->k))) return rc;
+  if (y == nullptr || y_stride < w->out || mid == nullptr || !aligned16(mid)) return MLORA_EINVAL;
+  const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
+  if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
+  return launch_base(w, *lora, *route, x, x_stride, y, y_stride, last_out, w->out, mid, gemv,
+                     static_cast<hipStream_t>(stream));
+}
+
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
                    int32_t k, uint16_t* y, int64_t y_stride, int32_t n_out, void* workspace, size_t workspace_bytes,
                    int32_t flags, void* stream) {

@@ -198,9 +198,9 @@ class Workspace:
                 raise ValueError("cu_seqlens must be a contiguous int32 tensor of requests + 1 offsets")
         if tokens > self.rows:
             raise ValueError(f"A pass of {tokens} tokens does not fit a workspace of {self.rows}")
-        key = (adp.data_ptr(), adp._version, requests, tokens, pool_rows,
-               None if cu_seqlens is None else (cu_seqlens.data_ptr(), cu_seqlens._version))
-        if self._routed == key and self._route_abi is not None:
+        key = (adp.data_ptr(), adp._version, requests, tokens, pool_rows)
+        seq = None if cu_seqlens is None else (cu_seqlens.data_ptr(), cu_seqlens._version)
+        if self._routed == (key, seq) and self._route_abi is not None:
             return self._route_abi
         r = _lib.Route(self.req_order.data_ptr(), self.tok_perm.data_ptr(), self.last_of.data_ptr(),
                        self.seg_start.data_ptr(), self.seg_adapter.data_ptr(), self.num_segs.data_ptr(),
@@ -209,13 +209,16 @@ class Workspace:
         stream = torch.cuda.current_stream(adp.device).cuda_stream
         _lib.check(h.mlora_route(adp.data_ptr(), 0 if cu_seqlens is None else cu_seqlens.data_ptr(),
                                  0 if cu_seqlens is not None else self.row_len, r, pool_rows, stream), "mlora_route")
-        self._routed = key
+        self._routed = (key, seq)
         self._route_abi = r
         return r
 
     def routed(self, adp: torch.Tensor, pool_rows: int, tokens: int) -> _lib.Route:
-        """The route of `adp` for a product of `tokens` tokens: the one already made for it in this workspace, else a
-        new one over uniform rows."""
+        """The route of `adp` for a product of `tokens` tokens: the one this workspace made last for the same adp
+        (uniform or ragged), else a new one over uniform rows."""
+        key = (adp.data_ptr(), adp._version, int(adp.numel()), tokens, pool_rows)
+        if self._routed is not None and self._routed[0] == key and self._route_abi is not None:
+            return self._route_abi
         return self.route(adp, pool_rows, tokens=tokens)
 
     def check(self) -> None:

@@ -59,3 +59,24 @@ def shrink(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, mfma: bo
     _lib.check(h.mlora_shrink(lin.lora_abi(), r, x.data_ptr(), x.stride(0), lin.k, ws.mid.data_ptr(), flags, stream),
                "mlora_shrink")
     return ws.mid[:m * lin.rank].view(m, lin.rank)
+
+
+def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: torch.Tensor,
+                tiles: Int4Tiles | None = None, last_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The second launch of int4_product alone, into a given y: the base product with the LoRA second factor fused,
+    reading the first factors the last shrink (or int4_product) of the same x and adp left in the workspace."""
+    packed = lin.int4
+    if packed is None:
+        raise ValueError(f"{', '.join(lin.names)}: no INT4 weights")
+    _check_input(lin, x, "the INT4 product")
+    m = x.shape[0]
+    if y.dtype != DT or tuple(y.shape) != (m, lin.out) or y.stride(1) != 1:
+        raise ValueError(f"y must be bfloat16 ({m}, {lin.out}) with contiguous rows")
+    r = ws.routed(adp, lin.pool.shape[0], m)
+    h = _lib.lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(h.mlora_int4_base_expand(packed.abi(), lin.lora_abi(), r, x.data_ptr(), x.stride(0), y.data_ptr(),
+                                        y.stride(0), 0 if last_out is None else last_out.data_ptr(),
+                                        ws.mid.data_ptr(), 0 if tiles is None else tiles.flags(), stream),
+               "mlora_int4_base_expand")
+    return y

@@ -19,7 +19,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from jeff_amd.fast_path import DT, AdapterPool, Lin, fold_scale
+from jeff_amd.fast_path import DT, AdapterPool, Lin
 from jeff_amd.int4 import KernelInt4, pack_kernel_asym
 
 HIDDEN, INTER, Q_OUT, KV_OUT = 2048, 6144, 16 * 128, 8 * 128
@@ -55,24 +55,27 @@ def _int4_weights(out: int, k: int, gen: torch.Generator, device: str, group: in
 
 
 def _fill_adapters(pool: AdapterPool, ranks: dict[int, int], gen: torch.Generator, device: str) -> None:
-    """Write random adapters straight into their pool rows: A ~ N(0, SIGMA_A), sB = bf16(2 B), B ~ N(0, SIGMA_B)."""
-    for row in sorted(ranks):
-        r = ranks[row]
-        name = f"adapter-{row}"
-        pool.adapter_index[name] = row
-        pool.free_rows.remove(row)
-        live: list[int] = []
-        for lin, offset in zip(pool.lins, pool.offsets):
-            flat = pool.lora_pool[row, offset:offset + lin.numel()]
-            a_view = flat[:lin.rank * lin.k].view(lin.rank, lin.k)
-            a_view.normal_(0.0, SIGMA_A, generator=gen)
-            for j, (size, cap) in enumerate(zip(lin.sizes, lin.caps)):
-                start = lin.off_bj[j] - lin.off_a
-                b_view = flat[start:start + size * cap].view(size, cap)
-                b = torch.empty(size, cap, device=device).normal_(0.0, SIGMA_B, generator=gen)
-                b_view.copy_(fold_scale(b, LORA_SCALE))
-                live.append(min(r, cap))
-        pool.ranks[row, :len(live)] = torch.tensor(live, dtype=torch.int32, device=device)
+    """Fill pool rows 1..n with random adapters, a whole group's block of rows at a time: A ~ N(0, SIGMA_A),
+    sB = 2 B with B ~ N(0, SIGMA_B) rounded to bf16 (doubling is exact, so this is bf16(2 B) as fold_scale gives)."""
+    rows = sorted(ranks)
+    assert rows == list(range(1, len(rows) + 1)), "adapters fill the rows after the base row in order"
+    n = len(rows)
+    for lin in pool.lins:
+        block = pool.lora_pool[1:n + 1, lin.off_a:lin.off_a + lin.numel()]
+        block[:, :lin.rank * lin.k].normal_(0.0, SIGMA_A, generator=gen)
+        b = block[:, lin.rank * lin.k:]
+        b.normal_(0.0, SIGMA_B, generator=gen)
+        b.mul_(LORA_SCALE)
+    r = torch.tensor([ranks[a] for a in rows], dtype=torch.int32, device=device)
+    col = 0
+    for lin in pool.lins:
+        for cap in lin.caps:
+            pool.ranks[1:n + 1, col] = torch.clamp(r, max=cap)
+            col += 1
+    for a in rows:
+        name = f"adapter-{a}"
+        pool.adapter_index[name] = a
+        pool.free_rows.remove(a)
 
 
 def _layers(n_layers: int, cap: int, gen: torch.Generator, device: str) -> list[dict[str, Lin]]:

@@ -12,6 +12,7 @@ from jeff_amd.fast_path import DT, AdapterPool, Lin, fold_scale
 from jeff_amd.int4 import pack_kernel, pack_kernel_asym
 from oracle import codec
 from oracle.layer import exact_and_bound, reference_f32, within_tolerance
+from oracle.pool_view import adapters_of
 from oracle.routing import token_adapters
 
 
@@ -66,25 +67,7 @@ def make_case(sizes: list[int], k: int, group: int, asym: bool, adapter_ranks: d
 
 def oracle_adapters(lin: Lin, rows) -> dict:
     """{pool row: [(A (r, k), sB (out_j, r)) or None per matrix]} read back from the device pool."""
-    out = {}
-    n = len(lin.names)
-    for row in rows:
-        row = int(row)
-        if row == 0:
-            continue
-        ranks = lin.ranks_table[row, lin.rank_col:lin.rank_col + n].cpu().tolist()
-        flat = lin.pool[row, lin.off_a:lin.off_a + lin.numel()].cpu()
-        a_all = flat[:lin.rank * lin.k].view(lin.rank, lin.k)
-        ups = []
-        for j, (size, cap, r) in enumerate(zip(lin.sizes, lin.caps, ranks)):
-            if r == 0:
-                ups.append(None)
-                continue
-            start = lin.off_bj[j] - lin.off_a
-            sb = flat[start:start + size * cap].view(size, cap)[:, :r].contiguous()
-            ups.append((a_all[lin.rho[j]:lin.rho[j] + r].contiguous(), sb))
-        out[row] = ups
-    return out
+    return adapters_of(lin, rows)
 
 
 def judge(lin: Lin, w: torch.Tensor, x: torch.Tensor, tok_adp: np.ndarray, got: torch.Tensor,
