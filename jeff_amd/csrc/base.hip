@@ -186,6 +186,7 @@ __global__ __launch_bounds__(256) void base_mfma_kernel(mlora_int4_t w, mlora_lo
 
 constexpr int kGvCols = 64, kGvSlices = 16;
 constexpr int kGvMaxTokens = 8;
+constexpr int kBigTileTokens = 1024;  // from here on the 256 x 256 tiles of gemm256.hip fill the chip
 
 template <bool kBase>
 __global__ __launch_bounds__(256) void base_gemv_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
@@ -277,6 +278,8 @@ int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_
     else
       hipLaunchKernelGGL(base_gemv_kernel<false>, dim3(blocks), dim3(256), 0, stream, none, L, r, x, x_stride, y,
                          y_stride, last_out, n_out, mid);
+  } else if (w != nullptr && r.tokens >= kBigTileTokens) {
+    return launch_base256(*w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, stream);
   } else {
     const int m_tiles = (int)((r.tokens + kBM - 1) / kBM);
     const int n_tiles = (n_out + kBN - 1) / kBN;

@@ -129,6 +129,9 @@ int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const m
 int launch_dequant(const mlora_int4_t& w, uint16_t* out, hipStream_t stream);
 int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x, int64_t x_stride, int32_t k,
                   uint16_t* mid, bool mfma, hipStream_t stream);
+int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
+                   int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+                   const uint16_t* mid, hipStream_t stream);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

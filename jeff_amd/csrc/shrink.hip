@@ -46,17 +46,18 @@ __global__ __launch_bounds__(kGemvThreads) void shrink_gemv_kernel(mlora_lora_t 
 #pragma unroll
     for (int i = 0; i < kGemvRows * kGemvRanks; ++i) v[i] = 0.0f;
     for (int i = tid; i < kw; i += kGemvThreads) {
-      uint4 xv[kGemvRows];
+      // every load is issued before any use (rank rows past the live rank re-read the last live row and are dropped),
+      // so the 4 + 16 requests of a thread are in flight together
+      uint4 xv[kGemvRows], av[kGemvRanks];
 #pragma unroll
       for (int rr = 0; rr < kGemvRows; ++rr) xv[rr] = *reinterpret_cast<const uint4*>(xr[rr] + 8 * i);
 #pragma unroll
-      for (int q = 0; q < kGemvRanks; ++q) {
-        if (q < nq) {
-          const uint4 av = *reinterpret_cast<const uint4*>(A + (int64_t)q * k + 8 * i);
+      for (int q = 0; q < kGemvRanks; ++q)
+        av[q] = *reinterpret_cast<const uint4*>(A + (int64_t)min(q, nq - 1) * k + 8 * i);
 #pragma unroll
-          for (int rr = 0; rr < kGemvRows; ++rr) v[rr * kGemvRanks + q] = dot8(xv[rr], av, v[rr * kGemvRanks + q]);
-        }
-      }
+      for (int q = 0; q < kGemvRanks; ++q)
+#pragma unroll
+        for (int rr = 0; rr < kGemvRows; ++rr) v[rr * kGemvRanks + q] = dot8(xv[rr], av[q], v[rr * kGemvRanks + q]);
     }
     // reduce-scatter across the wave: afterwards lane l holds the wave's sum of value l (row l/16, rank l%16)
 #pragma unroll
@@ -80,96 +81,123 @@ __global__ __launch_bounds__(kGemvThreads) void shrink_gemv_kernel(mlora_lora_t 
   }
 }
 
-constexpr int kSM = 64;          // sorted positions per workgroup
-constexpr int kSK = 64;          // inputs per staged chunk
-constexpr int kSLd = kSK + 8;    // LDS row stride in bf16 (144 bytes: 16-byte reads of 32 rows hit distinct banks)
-constexpr int kJobsPerWave = 2;  // (row block, matrix, 32-rank block) accumulators per wave and round
+constexpr int kSM = 64;         // sorted positions per workgroup: 2 row blocks of 32
+constexpr int kSK = 64;         // inputs per step
+constexpr int kSLd = kSK + 8;   // LDS row stride in bf16 (144 bytes: 16-byte reads of 32 rows hit distinct banks)
+constexpr int kMaxBlocks = 8;   // 32-rank blocks per pass (256 ranks)
 
+// The (matrix, 32-rank block) of block index b of an adapter whose live ranks are rk[].
+__device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int& j, int& kb) {
+  j = 0;
+  while (j + 1 < n_mats && b >= ((rk[j] + 31) >> 5)) {
+    b -= (rk[j] + 31) >> 5;
+    ++j;
+  }
+  kb = b;
+}
+
+// One workgroup per 64 sorted positions and every segment crossing them: x rows and the segment's A rows are staged
+// through double-buffered LDS (the next step's loads in flight while the MFMAs run, one barrier per step); waves
+// (row block rb, half) take the rank blocks of their half.
 __global__ __launch_bounds__(256) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
                                                          const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
                                                          uint16_t* __restrict__ mid) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kSM * kSLd];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kSM * kSLd];
+  __shared__ __attribute__((aligned(16))) uint16_t as[2][kMaxBlocks * 32 * kSLd];
   const int64_t T = r.tokens;
   const int64_t p0 = (int64_t)blockIdx.x * kSM;
   if (p0 >= T) return;
   const int nseg = *r.num_segs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rb = wave & 1, half = wave >> 1;
   const int64_t tile_end = min(p0 + kSM, T);
-  const int srow = tid >> 2, scol = (tid & 3) * 16;  // staging: 16 inputs of one row per thread
+  const int srow = tid >> 2, scol = (tid & 3) * 16;  // x staging: 16 inputs of one row
+  const int arow = tid >> 3, acol = (tid & 7) * 8;   // A staging: 8 inputs of one rank row per block
   const int64_t sp = p0 + srow;
+  const int nk = k / kSK;
   for (int s = segment_of(r.seg_start, nseg, p0); s < nseg && r.seg_start[s] < tile_end; ++s) {
     const int64_t sb = max((int64_t)r.seg_start[s], p0), se = min((int64_t)r.seg_start[s + 1], tile_end);
     if (se <= sb) continue;
     const int a = r.seg_adapter[s];
-    int rank[MLORA_MAX_MATS];
-    int blocks_total = 0;
+    int rk[MLORA_MAX_MATS];
+    int nblk = 0;
     for (int j = 0; j < L.n_mats; ++j) {
-      rank[j] = live_rank(L, a, j);
-      blocks_total += (rank[j] + 31) >> 5;
+      rk[j] = live_rank(L, a, j);
+      nblk += (rk[j] + 31) >> 5;
     }
-    const int rb_lo = (int)((sb - p0) >> 5), rb_hi = (int)((se - 1 - p0) >> 5);
-    const int njobs = (rb_hi - rb_lo + 1) * blocks_total;
-    if (njobs == 0) continue;
-    const bool stage = sp >= sb && sp < se;
-    const uint16_t* xsrc = stage ? x + (int64_t)r.tok_perm[sp] * x_stride + scol : nullptr;
+    if (nblk == 0) continue;
+    const uint16_t* xsrc = (sp >= sb && sp < se) ? x + (int64_t)r.tok_perm[sp] * x_stride + scol : nullptr;
     const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a;
-    for (int round = 0; round < njobs; round += 4 * kJobsPerWave) {
-      f32x16_t acc[kJobsPerWave];
-      int jrow[kJobsPerWave], jmat[kJobsPerWave], jn[kJobsPerWave];
-      bool jok[kJobsPerWave];
-      const uint16_t* arow[kJobsPerWave];
+    for (int b0 = 0; b0 < nblk; b0 += kMaxBlocks) {
+      const int nbp = min(kMaxBlocks, nblk - b0);
+      const uint16_t* asrc[kMaxBlocks];
 #pragma unroll
-      for (int jj = 0; jj < kJobsPerWave; ++jj) {
-        acc[jj] = f32x16_t{};
-        const int job = round + wave + 4 * jj;
-        jok[jj] = job < njobs;
-        int rbi = 0, j = 0, kb = 0;
-        if (jok[jj]) {
-          rbi = job / blocks_total;
-          int b = job - rbi * blocks_total;
-          while (b >= ((rank[j] + 31) >> 5)) {
-            b -= (rank[j] + 31) >> 5;
-            ++j;
-          }
-          kb = b;
+      for (int bi = 0; bi < kMaxBlocks; ++bi) {
+        asrc[bi] = nullptr;
+        if (bi < nbp) {
+          int j, kb;
+          rank_block(rk, L.n_mats, b0 + bi, j, kb);
+          const int n = kb * 32 + arow;
+          if (n < rk[j]) asrc[bi] = Abase + (int64_t)(rank_offset(L, j) + n) * k + acol;
         }
-        jrow[jj] = (rb_lo + rbi) * 32;
-        jmat[jj] = j;
-        jn[jj] = kb * 32 + (lane & 31);  // this lane's rank (MFMA column)
-        const bool nok = jok[jj] && jn[jj] < rank[j];
-        arow[jj] = nok ? Abase + (int64_t)(rank_offset(L, j) + jn[jj]) * k : nullptr;
       }
-      for (int kc = 0; kc < k; kc += kSK) {
-        __syncthreads();
-        uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
+      uint4 xv[2], av[kMaxBlocks];
+      auto fetch = [&](int kc) {
+        xv[0] = xv[1] = make_uint4(0, 0, 0, 0);
         if (xsrc != nullptr) {
-          v0 = *reinterpret_cast<const uint4*>(xsrc + kc);
-          v1 = *reinterpret_cast<const uint4*>(xsrc + kc + 8);
+          xv[0] = *reinterpret_cast<const uint4*>(xsrc + kc);
+          xv[1] = *reinterpret_cast<const uint4*>(xsrc + kc + 8);
         }
-        *reinterpret_cast<uint4*>(&xs[srow * kSLd + scol]) = v0;
-        *reinterpret_cast<uint4*>(&xs[srow * kSLd + scol + 8]) = v1;
-        __syncthreads();
 #pragma unroll
-        for (int jj = 0; jj < kJobsPerWave; ++jj) {
-          if (!jok[jj]) continue;
+        for (int bi = 0; bi < kMaxBlocks; ++bi)
+          av[bi] = asrc[bi] != nullptr ? *reinterpret_cast<const uint4*>(asrc[bi] + kc) : make_uint4(0, 0, 0, 0);
+      };
+      auto stage = [&](int buf) {
+        *reinterpret_cast<uint4*>(&xs[buf][srow * kSLd + scol]) = xv[0];
+        *reinterpret_cast<uint4*>(&xs[buf][srow * kSLd + scol + 8]) = xv[1];
 #pragma unroll
-          for (int k16 = 0; k16 < kSK / 16; ++k16) {
-            const int kk = k16 * 16 + (lane >> 5) * 8;
-            const uint4 av = *reinterpret_cast<const uint4*>(&xs[(jrow[jj] + (lane & 31)) * kSLd + kk]);
-            const uint4 bv = arow[jj] != nullptr ? *reinterpret_cast<const uint4*>(arow[jj] + kc + kk)
-                                                  : make_uint4(0, 0, 0, 0);
-            acc[jj] = mfma32(av, bv, acc[jj]);
+        for (int bi = 0; bi < kMaxBlocks; ++bi)
+          if (bi < nbp) *reinterpret_cast<uint4*>(&as[buf][(bi * 32 + arow) * kSLd + acol]) = av[bi];
+      };
+      f32x16_t acc[kMaxBlocks / 2];
+#pragma unroll
+      for (int m = 0; m < kMaxBlocks / 2; ++m) acc[m] = f32x16_t{};
+      fetch(0);
+      stage(0);
+      if (nk > 1) fetch(kSK);
+      __syncthreads();
+      for (int it = 0; it < nk; ++it) {
+        const int cur = it & 1;
+#pragma unroll
+        for (int k16 = 0; k16 < kSK / 16; ++k16) {
+          const int kk = k16 * 16 + (lane >> 5) * 8;
+          const uint4 av16 = *reinterpret_cast<const uint4*>(&xs[cur][(rb * 32 + (lane & 31)) * kSLd + kk]);
+#pragma unroll
+          for (int m = 0; m < kMaxBlocks / 2; ++m) {
+            const int bi = half + 2 * m;
+            if (bi < nbp) {
+              const uint4 bv = *reinterpret_cast<const uint4*>(&as[cur][(bi * 32 + (lane & 31)) * kSLd + kk]);
+              acc[m] = mfma32(av16, bv, acc[m]);
+            }
           }
         }
+        if (it + 1 < nk) stage(cur ^ 1);
+        if (it + 2 < nk) fetch((it + 2) * kSK);
+        __syncthreads();
       }
 #pragma unroll
-      for (int jj = 0; jj < kJobsPerWave; ++jj) {
-        if (!jok[jj] || jn[jj] >= rank[jmat[jj]]) continue;
-        uint16_t* out = mid + rank_offset(L, jmat[jj]) + jn[jj];
+      for (int m = 0; m < kMaxBlocks / 2; ++m) {
+        const int bi = half + 2 * m;
+        if (bi >= nbp) continue;
+        int j, kb;
+        rank_block(rk, L.n_mats, b0 + bi, j, kb);
+        const int n = kb * 32 + (lane & 31);
+        if (n >= rk[j]) continue;
+        uint16_t* out = mid + rank_offset(L, j) + n;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int64_t p = p0 + jrow[jj] + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if (p >= sb && p < se) out[p * L.rank_cap] = f32_to_bf16(acc[jj][i]);
+          const int64_t p = p0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if (p >= sb && p < se) out[p * L.rank_cap] = f32_to_bf16(acc[m][i]);
         }
       }
     }

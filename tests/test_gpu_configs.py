@@ -1,0 +1,78 @@
+"""The five benchmark configurations at their real shapes on the GPU, checked against the CPU oracle.
+
+Each output row depends only on its own input row, the group's weights and its adapter, so checking a sample of rows
+(every request's first and last token among them) with the oracle is an exact check of those rows; the whole output
+is checked for finiteness. The decoder configurations run one of their 28 identical layers (all four fused groups).
+- cpu-1024: bf16 base 1024 -> 1024 (torch's GEMM, the reference's "cublas" product) plus lora_add, 256 tokens in 8
+  segments of 32, 4 adapters of rank 16;
+- prefill-1layer, decode-28l, prefill-skewed-28l (with the last-token gather), decode-pool-28l: int4_product."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from jeff_amd import workloads
+from jeff_amd.fast_path import DT, AdapterPool, Lin, Workspace, fold_scale, lora_add
+from jeff_amd.int4_kernels import int4_product
+from oracle.layer import exact_and_bound, reference_f32, step, uncut_bound, within_tolerance
+from oracle.pool_view import adapters_of, weights_of
+from tests.gpu_cases import judge
+
+pytestmark = pytest.mark.gpu
+
+
+def test_cpu_reference_config_bf16_base() -> None:
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(256, 1024, generator=g).to(DT)
+    w = (torch.randn(1024, 1024, generator=g) * 0.02).to(DT)
+    lin = Lin(["layers.0.self_attn.o_proj"], [w.cuda()])
+    pool = AdapterPool([lin], 4)
+    for a in range(1, 5):
+        am = (torch.randn(16, 1024, generator=g) / 32).to(DT)
+        b = torch.randn(1024, 16, generator=g) * 0.02
+        pool.add_adapter(f"a{a}", {lin.names[0]: (am.cuda(), fold_scale(b, 2.0).cuda())})
+    ids = torch.randint(1, 5, (8,), generator=g).to(torch.int32)
+    ws = Workspace(256, 32, max_rank=lin.rank)
+    got = lin(x.cuda(), ws, ids.cuda()).cpu()
+    tok = np.repeat(ids.numpy(), 32)
+    adapters = adapters_of(lin, np.unique(tok))
+    exact, bound = exact_and_bound(x, w, tok, adapters, lin.sizes, lin.rank)
+    allowed = uncut_bound(x, w, exact, bound) + step(exact.abs())  # torch's GEMM orders its sums its own way
+    assert int(((got.double() - exact).abs() > allowed).sum()) == 0
+    assert bool(within_tolerance(got, reference_f32(x, w, tok, adapters, lin.sizes)).all())
+
+
+def sample_rows(w: workloads.Workload, n_random: int = 48) -> np.ndarray:
+    cu = np.concatenate([[0], np.cumsum(w.lengths)])
+    rng = np.random.default_rng(7)
+    firsts = cu[:-1][w.lengths > 0]
+    lasts = cu[1:][w.lengths > 0] - 1
+    picks = rng.choice(len(firsts), min(24, len(firsts)), replace=False)
+    rows = np.concatenate([firsts[picks], lasts[picks], rng.integers(0, w.tokens, n_random)])
+    return np.unique(rows)
+
+
+@pytest.mark.parametrize("name", ["prefill-1layer", "decode-28l", "prefill-skewed-28l", "decode-pool-28l"])
+def test_config_at_full_shape(name: str) -> None:
+    w = workloads.make(name, n_layers=1)
+    layer = w.layers[0]
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    ws = Workspace(w.tokens, 1, max_rank=max(lin.rank for lin in layer.values()), max_requests=w.requests)
+    ws.route(w.adp, w.pool.lora_pool.shape[0], tokens=w.tokens, cu_seqlens=w.cu_seqlens)
+    tok = workloads.token_ids(w)
+    rows = sample_rows(w)
+    for label, lin in layer.items():
+        x = workloads.inputs(w, label, gen)
+        last = torch.empty(w.requests, lin.out, dtype=DT, device="cuda") if w.gather_last else None
+        y = int4_product(lin, x, ws, w.adp, last_out=last)
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(y.float()).all()), f"{name} {label}: non-finite outputs"
+        if last is not None:
+            ends = torch.as_tensor(np.cumsum(w.lengths) - 1, device="cuda")
+            assert torch.equal(last, y[ends]), f"{name} {label}: gathered rows differ"
+        r = judge(lin, weights_of(lin.int4), x, tok, y, rows=rows)
+        assert r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, f"{name} {label}: {r}"
+        del x, y, last
+    ws.check()
