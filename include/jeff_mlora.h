@@ -82,6 +82,7 @@ typedef struct {
  *   req_order (requests)        request rows in sorted order
  *   tok_perm  (tokens)          sorted token position -> original token index
  *   last_of   (tokens)          per sorted position, the request whose last token is there, else -1
+ *   seg_of    (tokens)          per sorted position, the segment it belongs to
  *   seg_start (max_segs + 1)    first sorted position of each segment, then the end
  *   seg_adapter (max_segs)      the pool row of each segment, increasing
  *   num_segs, status (1 each)   the number of segments; MLORA_ROUTE_* bits
@@ -90,6 +91,7 @@ typedef struct {
   int32_t* req_order;
   int32_t* tok_perm;
   int32_t* last_of;
+  int32_t* seg_of;
   int32_t* seg_start;
   int32_t* seg_adapter;
   int32_t* num_segs;

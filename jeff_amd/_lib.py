@@ -44,7 +44,8 @@ class Lora(ctypes.Structure):
 
 
 class Route(ctypes.Structure):
-    _fields_ = [("req_order", c_vp), ("tok_perm", c_vp), ("last_of", c_vp), ("seg_start", c_vp),
+    _fields_ = [("req_order", c_vp), ("tok_perm", c_vp), ("last_of", c_vp), ("seg_of", c_vp),
+                ("seg_start", c_vp),
                 ("seg_adapter", c_vp), ("num_segs", c_vp), ("status", c_vp), ("tokens", c_i64),
                 ("requests", c_i32), ("max_segs", c_i32)]
 

@@ -15,7 +15,7 @@ int check_route(const mlora_route_t* r) {
   if (r->requests > MLORA_MAX_REQUESTS) return MLORA_EUNSUPPORTED;
   if (r->num_segs == nullptr || r->seg_start == nullptr || r->seg_adapter == nullptr || r->status == nullptr)
     return MLORA_EINVAL;
-  if (r->tokens > 0 && (r->tok_perm == nullptr || r->last_of == nullptr)) return MLORA_EINVAL;
+  if (r->tokens > 0 && (r->tok_perm == nullptr || r->last_of == nullptr || r->seg_of == nullptr)) return MLORA_EINVAL;
   if (r->requests > 0 && r->req_order == nullptr) return MLORA_EINVAL;
   return MLORA_OK;
 }

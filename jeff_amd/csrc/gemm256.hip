@@ -1,24 +1,25 @@
 // Prefill-sized INT4 base product with the LoRA second factor fused (the same arithmetic as base.hip's kernels):
 //   y[perm[p], c] = bf16( sum_k x[perm[p], k] W[c, k] + sum_q mid[p, rho_j + q] sB_j[a][c - o_j, q] )
 // Tiles of 256 sorted tokens x 256 columns, 8 waves of 128 x 64 (2 x 4), 32x32x16 bf16 MFMA, float32 accumulators;
-// two waves per SIMD.
+// two waves per SIMD. The MFMAs take the weights as their first operand, so each lane's accumulators hold four
+// consecutive output columns of one token row.
 //
 // Per K step of 64 inputs:
-//  - x: the 256 gathered rows go straight from memory to LDS with global_load_lds (16 bytes per lane, no registers),
-//    two steps ahead, into a ring of three LDS buffers; the waves read their A operands from it;
-//  - weights: no LDS at all. Each lane loads the packed words that form its own B operands (one 32-bit word = the 8
+//  - x: the 256 gathered rows go straight from memory to LDS (buffer loads with the LDS flag, 16 bytes per lane, no
+//    registers), two steps ahead, into a ring of three LDS buffers; the waves read their operands from it;
+//  - weights: no LDS at all. Each lane loads the packed words that form its own operands (one 32-bit word = the 8
 //    consecutive inputs of one column that a 32x32x16 operand lane holds), one step ahead, with the raw scale and
-//    zero point of its columns, and dequantises them to bf16((c - z) s) in registers right before the MFMAs. The two
-//    waves sharing a column range both dequantise it, which costs VALU time that their MFMAs hide.
-// With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: a plain s_barrier after an
+//    zero point of its columns, and dequantises them to bf16((c - z) s) in registers, the next 16 inputs' words
+//    interleaved with the current MFMAs. The two waves sharing a column range both dequantise it.
+// With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: an LDS-only barrier after an
 // explicit wait for the x rows of the next step (a __syncthreads() would also wait for the rows two steps ahead).
-// LDS rows are 128 bytes (64 bf16) with their eight 16-byte chunks XOR-swizzled by (row & 7): the 16-byte A-operand
+// LDS rows are 128 bytes (64 bf16) with their eight 16-byte chunks XOR-swizzled by (row & 7): the 16-byte operand
 // reads of 8 consecutive rows hit 8 distinct chunk positions, i.e. all banks once. The ring buffers are distinct LDS
-// arrays chosen at compile time (the loop is unrolled by three). Tiles are ordered so that the column tiles of one
+// arrays chosen at compile time (the loop is unrolled by six). Tiles are ordered so that the column tiles of one
 // row tile run on the same XCD (its x rows, the larger operand, then come from that XCD's L2).
-// Epilogue: each adapter segment crossing the tile has its sB rows for the tile's 256 columns staged in LDS with
-// coalesced 16-byte loads and added by MFMA with the tokens' first factors (zero outside the segment), then the
-// single rounding to bf16.
+// Epilogue: the tile's first factors (sorted rows) are staged in LDS; each adapter segment crossing the tile adds
+// its sB rows (loaded straight into operands, one segment ahead) times the first factors of its rows by MFMA; then
+// the single rounding to bf16, staged through LDS so every output row is written in whole 512-byte pieces.
 #include <type_traits>
 
 #include "mlora_common.h"
@@ -38,6 +39,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 __shared__ __attribute__((aligned(16))) uint16_t g_x0[kTM * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t g_x1[kTM * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t g_x2[kTM * kTK];
+__shared__ int32_t g_orig[kTM];  // the tile's rows: original token index, -1 past the tokens
+__shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it is, else -1
 
 // Element offset of 16-byte chunk c of row `row` in a swizzled 64-element-per-row tile.
 __device__ __forceinline__ int swz(int row, int c) { return row * kTK + ((c ^ (row & 7)) << 3); }
@@ -45,6 +48,13 @@ __device__ __forceinline__ int swz(int row, int c) { return row * kTK + ((c ^ (r
 // Wait until at most n vector memory instructions of this wave are outstanding and its LDS operations are done
 // (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
 #define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+
+// Workgroup barrier that orders LDS accesses only (global stores in flight are not waited for).
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // blockIdx -> tile index such that consecutive tiles share an XCD (blocks are dealt to the 8 XCDs round-robin)
 __device__ __forceinline__ int xcd_tile(int b, int nb) {
@@ -64,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
-                                                               const uint16_t* __restrict__ mid, int32_t n_tiles) {
+                                                               const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
   const int t = xcd_tile(blockIdx.x, gridDim.x);
@@ -81,6 +91,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)w.words, (short)0, (int)((int64_t)(w.k / 8) * w.columns * 4), 0x00020000);
   const int64_t groups = w.k / w.group;
+  const int gshift = w.group == 128 ? 7 : 6;  // the host accepts groups of 64 and 128 inputs
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)w.scales, (short)0, (int)(groups * w.columns * 2), 0x00020000);
   const bool asym = w.zeros != nullptr;
@@ -89,6 +100,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
   // x: instruction i of wave `wave` fills rows (8 i + wave) * 8 .. +7; lane l writes LDS chunk slot l & 7 of row
   // +(l >> 3), which holds logical chunk (l & 7) ^ (l >> 3). Rows past the tokens read row 0 of the pass.
+  if (tid < kTM) {
+    const int64_t p = p0 + tid;
+    g_orig[tid] = p < T ? r.tok_perm[p] : -1;
+    g_last[tid] = (p < T && last_out != nullptr) ? r.last_of[p] : -1;
+  }
   uint32_t xoff[kXLoads];
 #pragma unroll
   for (int i = 0; i < kXLoads; ++i) {
@@ -124,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 #pragma unroll
       for (int k16 = 0; k16 < 4; ++k16)
         st.w[nb][k16] = __builtin_amdgcn_raw_buffer_load_b32(wres, woff[nb], wbase + k16 * wstep, 0);
-    const int g = (kc / w.group) * w.columns;
+    const int g = (kc >> gshift) * w.columns;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       st.sbits[nb] = __builtin_amdgcn_raw_buffer_load_b16(sres, soff[nb], g * 2, 0);
@@ -144,8 +160,9 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     for (int mb = 0; mb < 4; ++mb)
       a[mb] = *reinterpret_cast<const uint4*>(&xs[swz(wm * 128 + mb * 32 + (lane & 31), c)]);
   };
-  // one K step: A operands from the x buffer (the next 16 inputs' read while the current ones are multiplied), B
-  // operands dequantised in registers from the step's words
+  // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. The A
+  // reads and the dequantisation of the next 16 inputs are interleaved with the current 16 inputs' MFMAs (one MFMA,
+  // then a few VALU instructions or an LDS read), so the matrix core works while the wave converts.
   auto step = [&](const uint16_t* xs, const WStage& ws) {
     float sv[2], zs[2];
 #pragma unroll
@@ -155,20 +172,33 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       sv[nb] = colok[nb] ? s0v : 0.0f;
       zs[nb] = colok[nb] ? zv * s0v : 0.0f;
     }
-    uint4 a0[4], a1[4];
+    uint4 a0[4], a1[4], b0[2], b1[2];
     load_a(xs, 0, a0);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) b0[nb] = dequant_word(ws.w[nb][0], sv[nb], zs[nb]);
 #pragma unroll
     for (int k16 = 0; k16 < kTK / 16; ++k16) {
       uint4 (&ca)[4] = (k16 & 1) ? a1 : a0;
       uint4 (&na)[4] = (k16 & 1) ? a0 : a1;
-      if (k16 + 1 < kTK / 16) load_a(xs, k16 + 1, na);
-      uint4 b[2];
+      uint4 (&cb)[2] = (k16 & 1) ? b1 : b0;
+      uint4 (&nbv)[2] = (k16 & 1) ? b0 : b1;
+      if (k16 + 1 < kTK / 16) {
+        load_a(xs, k16 + 1, na);
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) b[nb] = dequant_word(ws.w[nb][k16], sv[nb], zs[nb]);
+        for (int nb = 0; nb < 2; ++nb) nbv[nb] = dequant_word(ws.w[nb][k16 + 1], sv[nb], zs[nb]);
+      }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(ca[mb], b[nb], acc[mb][nb]);
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(cb[nb], ca[mb], acc[mb][nb]);
+      if (k16 + 1 < kTK / 16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+          if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+      }
     }
   };
 
@@ -182,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   fetch_w(s0, 0);
   dma_x(g_x1, min(1, nk - 1) * kTK);
   MLORA_WAIT_VM(kWLoads + kXLoads);  // x(0) has landed
-  __builtin_amdgcn_s_barrier();
+  lds_sync();
   auto run = [&](auto xb, auto wb, int i) {
     constexpr int XB = decltype(xb)::value, WB = decltype(wb)::value;
     const uint16_t* xs = XB == 0 ? g_x0 : XB == 1 ? g_x1 : g_x2;
@@ -193,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     fetch_w(nxt, min(i + 1, nk - 1) * kTK);
     step(xs, cur);
     MLORA_WAIT_VM(kWLoads + kXLoads + kWLoads);  // x(i + 1) has landed
-    __builtin_amdgcn_s_barrier();
+    lds_sync();
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -212,97 +242,139 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     run(I2{}, I1{}, it + 5);
   }
   MLORA_WAIT_VM(0);
-  __builtin_amdgcn_s_barrier();
+  lds_sync();
 
-  // LoRA second factor, one adapter segment at a time; sB rows are staged in g_x0 (swizzled like x)
-  const int nseg = *r.num_segs;
-  const int64_t tile_end = min(p0 + kTM, T);
-  uint16_t* bl = g_x0;
-  const int wcol = tid & (kTN - 1), wh = tid >> 8;
-  for (int s = segment_of(r.seg_start, nseg, p0); s < nseg && r.seg_start[s] < tile_end; ++s) {
-    const int a = r.seg_adapter[s];
-    if (a == 0) continue;  // the base row: no update
-    const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
-    int rk[MLORA_MAX_MATS];
-    int maxr = 0;
-    const int jfirst = matrix_of(L, n0), jlast = matrix_of(L, min(n0 + kTN, n_out) - 1);
-    for (int j = 0; j < L.n_mats; ++j) {
-      rk[j] = live_rank(L, a, j);
-      if (j >= jfirst && j <= jlast) maxr = max(maxr, rk[j]);
-    }
-    const uint16_t* prow = L.pool + (int64_t)a * L.pool_stride;
-    for (int rc = 0; rc < maxr; rc += kRankChunk) {
-      const int gc = n0 + wcol;  // ranks rc + 32 h .. +31 of one column per thread
-      uint4 v[4];
+  // LoRA second factor. The tile's rows of the first factor (sorted order, ranks rc .. rc + 63 of matrix j) are
+  // staged in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come
+  // straight from memory as MFMA operands (the next segment's issued before the current one's products), and the
+  // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
+  // set to zero.
+  if (L.n_mats > 0 && mid != nullptr) {
+    const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kTM, T) - 1];
+    const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)mid, (short)0, (int)(T * L.rank_cap * 2), 0x00020000);
+    const int jlo = matrix_of(L, n0), jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
+    for (int j = jlo; j <= jhi; ++j) {
+      const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
+      // columns of the wave's two blocks inside matrix j (others get zero operands)
+      bool cin[2];
+      int64_t boff[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = make_uint4(0, 0, 0, 0);
-      if (gc < n_out) {
-        const int j = matrix_of(L, gc);
-        const uint16_t* src = prow + L.off_b[j] + (int64_t)(gc - col_offset(L, j)) * L.cap[j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kk = rc + (4 * wh + i) * 8;
-          if (kk < rk[j]) v[i] = keep_first(*reinterpret_cast<const uint4*>(src + kk), rk[j] - kk);
-        }
+      for (int nb = 0; nb < 2; ++nb) {
+        const int cc = n0 + wn * 64 + nb * 32 + (lane & 31);
+        cin[nb] = cc >= oj && cc < oj + cj && cc < n_out;
+        boff[nb] = L.off_b[j] + (int64_t)((cin[nb] ? cc : oj) - oj) * capj;
       }
-      __syncthreads();  // the previous pass (or the main loop) is done with bl
+      for (int rc = 0; rc < capj; rc += kRankChunk) {
+        // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
+        lds_sync();  // every wave is done with the previous chunk's rows
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&bl[swz(wcol, 4 * wh + i)]) = v[i];
-      __syncthreads();
+        for (int i = 0; i < kXLoads; ++i) {
+          const int row = (8 * i + wave) * 8 + (lane >> 3);
+          const uint32_t off =
+              (uint32_t)(((p0 + row) * L.rank_cap + rho + rc + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)(g_x0 + (8 * i + wave) * 8 * kTK), 16, off, 0, 0,
+                                                   0);
+        }
+        // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
+        auto load_b = [&](int s, uint4 (&bv)[2][4], int& rk) {
+          const int a = r.seg_adapter[s];
+          rk = a == 0 ? 0 : min(live_rank(L, a, j) - rc, kRankChunk);
+          const uint16_t* prow = L.pool + (int64_t)a * L.pool_stride;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int64_t r0 = p0 + wm * 128 + mb * 32;
-        if (r0 >= se || r0 + 32 <= sb || r0 >= T) continue;
-        const int64_t row = r0 + (lane & 31);
-        const bool rowok = row >= sb && row < se;
+          for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int c0 = n0 + wn * 64 + nb * 32;
-          if (c0 >= n_out) continue;
-          const int cc = c0 + (lane & 31);
-          const int jlo = matrix_of(L, c0), jhi = matrix_of(L, min(c0 + 31, n_out - 1));
-          for (int j = jlo; j <= jhi; ++j) {
-            const int rj = rk[j];
-            if (rj <= rc) continue;
-            const int oj = col_offset(L, j);
-            const bool colok2 = cc >= oj && cc < oj + L.cols[j] && cc < n_out;
-            const uint16_t* mrow = mid + (rowok ? row : 0) * L.rank_cap + rank_offset(L, j);
-            const int kend = min(rj, rc + kRankChunk);
-            for (int k0 = rc; k0 < kend; k0 += 16) {
-              const int kk = k0 + (lane >> 5) * 8;
-              const int nvalid = rj - kk;
-              uint4 av = make_uint4(0, 0, 0, 0), bv = av;
-              if (nvalid > 0) {
-                if (rowok) av = keep_first(*reinterpret_cast<const uint4*>(mrow + kk), nvalid);
-                if (colok2) bv = *reinterpret_cast<const uint4*>(&bl[swz(cc - n0, (kk - rc) >> 3)]);
-              }
-              acc[mb][nb] = mfma32(av, bv, acc[mb][nb]);
+            for (int k16 = 0; k16 < 4; ++k16) {
+              const int kk = 16 * k16 + 8 * (lane >> 5);
+              const int q = min(rc + kk, capj - 8);
+              bv[nb][k16] = *reinterpret_cast<const uint4*>(prow + boff[nb] + q);
+            }
+        };
+        auto apply = [&](int s, uint4 (&bv)[2][4], int rk) {
+          if (rk <= 0) return;
+          const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16)
+              bv[nb][k16] = cin[nb] ? keep_first(bv[nb][k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            const int64_t r0 = p0 + wm * 128 + mb * 32;
+            if (r0 >= se || r0 + 32 <= sb) continue;
+            const int64_t row = r0 + (lane & 31);
+            const bool rin = row >= sb && row < se;
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) {
+              if (16 * k16 >= rk) break;
+              uint4 av = *reinterpret_cast<const uint4*>(
+                  &g_x0[swz(wm * 128 + mb * 32 + (lane & 31), 2 * k16 + (lane >> 5))]);
+              av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+              for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(bv[nb][k16], av, acc[mb][nb]);
             }
           }
+        };
+        uint4 b0[2][4], b1[2][4];
+        int rk0, rk1;
+        load_b(s_lo, b0, rk0);
+        MLORA_WAIT_VM(8);  // the first factors have landed (the 8 sB loads may still be in flight)
+        lds_sync();
+        for (int s = s_lo; s <= s_hi; s += 2) {
+          load_b(min(s + 1, s_hi), b1, rk1);
+          apply(s, b0, rk0);
+          if (s + 1 > s_hi) break;
+          load_b(min(s + 2, s_hi), b0, rk0);
+          apply(s + 1, b1, rk1);
         }
       }
     }
   }
 
+  // Single rounding to bf16 and the stores, through LDS one half of the tile (128 rows, one wave row) at a time:
+  // lane l holds, for row mb * 32 + (l & 31) of its wave's rows, the four consecutive columns 8 g + 4 (l >> 5) .. +3
+  // of each 32-column block; it writes them to LDS (columns 0..127 of the tile in g_x0, 128..255 in g_x1, 256-byte
+  // rows with their 16-byte chunks XOR-swizzled by (row & 15)), then every thread reads 16-byte chunks back and
+  // writes whole 512-byte tile rows to the token's output row (and to its request's last-token row).
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    int32_t orig[16], lastq[16];
+  for (int half = 0; half < 2; ++half) {
+    lds_sync();  // every wave is done reading LDS
+    if (wm == half) {
+      uint16_t* buf = (wn >> 1) ? g_x1 : g_x0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t p = p0 + wm * 128 + mb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      orig[i] = p < T ? r.tok_perm[p] : -1;
-      lastq[i] = (p < T && last_out != nullptr) ? r.last_of[p] : -1;
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int row = mb * 32 + (lane & 31);
+            const int col = (wn & 1) * 64 + nb * 32 + g * 8 + (lane >> 5) * 4;
+            const uint32_t lo = pack_bf16x2(acc[mb][nb][4 * g], acc[mb][nb][4 * g + 1]);
+            const uint32_t hi = pack_bf16x2(acc[mb][nb][4 * g + 2], acc[mb][nb][4 * g + 3]);
+            *reinterpret_cast<uint2*>(&buf[row * 128 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)]) =
+                make_uint2(lo, hi);
+          }
     }
+    lds_sync();
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int c = n0 + wn * 64 + nb * 32 + (lane & 31);
-      if (c >= n_out) continue;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if (orig[i] < 0) continue;
-        const uint16_t v = f32_to_bf16(acc[mb][nb][i]);
-        y[(int64_t)orig[i] * y_stride + c] = v;
-        if (lastq[i] >= 0) last_out[(int64_t)lastq[i] * n_out + c] = v;
+    for (int i = 0; i < 8; ++i) {
+      const int f = tid + kThreads * i;
+      const int row = f >> 5, bsel = (f >> 4) & 1, c = f & 15;
+      const int64_t orig = g_orig[half * 128 + row];
+      if (orig < 0) continue;
+      const int64_t lq = g_last[half * 128 + row];
+      const uint4 v = *reinterpret_cast<const uint4*>(&(bsel ? g_x1 : g_x0)[row * 128 + ((c ^ (row & 15)) << 3)]);
+      const int col = n0 + bsel * 128 + c * 8;
+      if (vec && col + 7 < n_out) {
+        *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
+        if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * n_out + col) = v;
+      } else {
+        const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; e < 8 && col + e < n_out; ++e) {
+          const uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
+          y[orig * y_stride + col + e] = h;
+          if (lq >= 0) last_out[lq * n_out + col + e] = h;
+        }
       }
     }
   }
@@ -317,7 +389,10 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
   const int m_tiles = (int)((r.tokens + kTM - 1) / kTM);
   const int n_tiles = (n_out + kTN - 1) / kTN;
   const int64_t blocks = (int64_t)m_tiles * n_tiles;
+  // 16-byte stores of eight columns need 16-byte aligned output rows
+  const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
+                   (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);
   hipLaunchKernelGGL(base_mfma256_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, w, L, r, x, x_stride, y,
-                     y_stride, last_out, n_out, mid, n_tiles);
+                     y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

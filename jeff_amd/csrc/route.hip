@@ -42,6 +42,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
                                                              mlora_route_t r, int32_t pool_rows) {
   __shared__ uint32_t keys[MLORA_MAX_REQUESTS];
   __shared__ int32_t pstart[MLORA_MAX_REQUESTS];
+  __shared__ int32_t segidx[MLORA_MAX_REQUESTS];  // segment of each sorted request
   __shared__ int32_t wave_sums[16];
   __shared__ int32_t status, seq_ok;
   const int tid = threadIdx.x;
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
     for (int64_t p = tid; p < T; p += kRouteThreads) {
       r.tok_perm[p] = (int32_t)p;
       r.last_of[p] = -1;
+      r.seg_of[p] = 0;
     }
     for (int i = tid; i < B; i += kRouteThreads) r.req_order[i] = i;
     if (tid == 0) {
@@ -137,6 +139,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
     if (i < B) {
       pstart[i] = run;
       r.req_order[i] = rho[e];
+      segidx[i] = first[e] ? seg : seg - 1;
       if (first[e]) {
         r.seg_adapter[seg] = ada[e];
         r.seg_start[seg] = run;
@@ -155,10 +158,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
     const int q = (int)(keys[i] & ((1u << kIndexBits) - 1));
     const int start = cu != nullptr ? cu[q] : q * row_len;
     const int l = cu != nullptr ? cu[q + 1] - cu[q] : row_len;
-    const int ps = pstart[i];
+    const int ps = pstart[i], sg = segidx[i];
     for (int t = lane; t < l; t += 64) {
       r.tok_perm[ps + t] = start + t;
       r.last_of[ps + t] = t == l - 1 ? q : -1;
+      r.seg_of[ps + t] = sg;
     }
   }
   if (tid == 0) *r.status = status;

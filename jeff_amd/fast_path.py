@@ -169,6 +169,7 @@ class Workspace:
         self.req_order = torch.empty(b, **i32)
         self.tok_perm = torch.empty(max(rows, 1), **i32)
         self.last_of = torch.empty(max(rows, 1), **i32)
+        self.seg_of = torch.empty(max(rows, 1), **i32)
         self.seg_start = torch.empty(b + 1, **i32)
         self.seg_adapter = torch.empty(b, **i32)
         self.num_segs = torch.zeros(1, **i32)
@@ -203,7 +204,7 @@ class Workspace:
         if self._routed == (key, seq) and self._route_abi is not None:
             return self._route_abi
         r = _lib.Route(self.req_order.data_ptr(), self.tok_perm.data_ptr(), self.last_of.data_ptr(),
-                       self.seg_start.data_ptr(), self.seg_adapter.data_ptr(), self.num_segs.data_ptr(),
+                       self.seg_of.data_ptr(), self.seg_start.data_ptr(), self.seg_adapter.data_ptr(), self.num_segs.data_ptr(),
                        self.status.data_ptr(), tokens, requests, max(min(requests, pool_rows), 1))
         h = _lib.lib()
         stream = torch.cuda.current_stream(adp.device).cuda_stream

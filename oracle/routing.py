@@ -23,6 +23,7 @@ def route(adp: np.ndarray, pool_rows: int, row_len: int | None = None,
       seg_start (S+1,) sorted token positions where each segment begins (and the end)
       seg_adapter (S,) the pool row of each segment, increasing; S = number of distinct adapters present
       last_of   (T,)   per sorted position: the request row whose last token sits there, else -1
+      seg_of    (T,)   per sorted position: the segment it lies in
       status    int    STATUS_BAD_ADAPTER if an index was out of range (those rows use row 0)"""
     adp = np.asarray(adp, dtype=np.int64)
     b = adp.shape[0]
@@ -51,7 +52,8 @@ def route(adp: np.ndarray, pool_rows: int, row_len: int | None = None,
     seg_start = np.concatenate([starts_sorted[first], [t]]) if b else np.zeros(1, dtype=np.int64)
     return {"req_order": order.astype(np.int32), "tok_perm": tok_perm.astype(np.int32),
             "seg_start": seg_start.astype(np.int32), "seg_adapter": seg_adapter.astype(np.int32),
-            "last_of": last_of.astype(np.int32), "status": status}
+            "last_of": last_of.astype(np.int32),
+            "seg_of": np.repeat(np.arange(seg_adapter.size), np.diff(seg_start)).astype(np.int32), "status": status}
 
 
 def token_adapters(adp: np.ndarray, pool_rows: int, row_len: int | None = None,

@@ -57,9 +57,9 @@ def test_workspace_bytes_and_refusals_before_any_launch() -> None:
     assert h.mlora_dequant(ctypes.byref(w), 16, None) == _lib.EUNSUPPORTED
     w = _lib.Int4(16, 16, None, 1000, 3072, 3072, 64)
     assert h.mlora_dequant(ctypes.byref(w), 16, None) == _lib.EINVAL
-    r = _lib.Route(0, 0, 0, 0, 0, 0, 0, 10, _lib.MAX_REQUESTS + 1, 1)
+    r = _lib.Route(0, 0, 0, 0, 0, 0, 0, 0, 10, _lib.MAX_REQUESTS + 1, 1)
     assert h.mlora_route(16, None, 1, ctypes.byref(r), 4, None) == _lib.EUNSUPPORTED
-    r = _lib.Route(16, 16, 16, 16, 16, 16, 16, 10, 10, 1)
+    r = _lib.Route(16, 16, 16, 16, 16, 16, 16, 16, 10, 10, 1)
     assert h.mlora_route(16, None, 1, ctypes.byref(r), 4, None) == _lib.EINVAL  # max_segs < min(requests, rows)
-    assert h.mlora_route(16, None, 2, ctypes.byref(_lib.Route(16, 16, 16, 16, 16, 16, 16, 10, 10, 4)), 4,
+    assert h.mlora_route(16, None, 2, ctypes.byref(_lib.Route(16, 16, 16, 16, 16, 16, 16, 16, 10, 10, 4)), 4,
                          None) == _lib.EINVAL  # 10 rows of 2 tokens are not 10 tokens

@@ -56,6 +56,7 @@ def assert_route_equal(ws: Workspace, tokens: int, want: dict, requests: int) ->
     assert np.array_equal(ws.req_order[:requests].cpu().numpy(), want["req_order"])
     assert np.array_equal(ws.tok_perm[:tokens].cpu().numpy(), want["tok_perm"])
     assert np.array_equal(ws.last_of[:tokens].cpu().numpy(), want["last_of"])
+    assert np.array_equal(ws.seg_of[:tokens].cpu().numpy(), want["seg_of"])
     assert int(ws.status.item()) == want["status"]
 
 
@@ -105,6 +106,7 @@ def test_route_flags_unusable_seqlens_and_falls_back_to_identity() -> None:
     ws, tokens = run_route(np.array([1, 2, 3]), 4, None, cu)
     assert int(ws.status.item()) == _lib.ROUTE_BAD_SEQLENS
     assert np.array_equal(ws.tok_perm[:tokens].cpu().numpy(), np.arange(tokens))
+    assert not ws.seg_of[:tokens].cpu().numpy().any()
     assert int(ws.num_segs.item()) == 1 and int(ws.seg_adapter[0].item()) == 0
     with pytest.raises(ValueError, match="cu_seqlens"):
         ws.check()

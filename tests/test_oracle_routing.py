@@ -23,6 +23,8 @@ def check_invariants(adp, pool_rows, row_len=None, cu=None):
         assert np.all(tok_adp[perm[ss[s]:ss[s + 1]]] == sa[s])           # a segment holds one adapter's tokens
         assert np.all(np.diff(perm[ss[s]:ss[s + 1]]) > 0)                 # stable: original order kept
     assert set(sa.tolist()) >= set(tok_adp.tolist())
+    so = r["seg_of"]                                                      # each position lies in its segment
+    assert so.size == t and np.all(ss[so] <= np.arange(t)) and np.all(np.arange(t) < ss[so + 1])
     last = r["last_of"]
     lengths = np.diff(cu) if cu is not None else np.full(len(adp), row_len)
     ends = (np.cumsum(lengths) - 1)
