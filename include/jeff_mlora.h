@@ -14,6 +14,7 @@
  *   mlora_int4_base_expand  the base tiles + LoRA output epilogue          int4_kernels.py:44-64,105-129
  *   mlora_dequant      dequantize / bf16(q * s) of the kernel layout       int4.py:203-208,258-262
  *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
+ *   mlora_int4_partials_bytes  Workspace.P sizing (split partial products)  int4_kernels.py:150-166
  */
 #ifndef JEFF_MLORA_H
 #define JEFF_MLORA_H
@@ -49,6 +50,7 @@ enum {
 #define MLORA_FORCE_BASE_MFMA 2
 #define MLORA_FORCE_SHRINK_GEMV 4
 #define MLORA_FORCE_SHRINK_MFMA 8
+#define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
 
 /* INT4 weights in the kernel layout (reference int4.py:215-230, plus zero points and g128):
  * words  int32 (k/8, columns): word i of column c holds inputs 8i..8i+7, input 8i+j in bits 4j..4j+3 (the code c);
@@ -118,18 +120,27 @@ int mlora_dequant(const mlora_int4_t* w, uint16_t* out, void* stream);
 int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
                  int32_t k, uint16_t* mid, int32_t flags, void* stream);
 
+/* Bytes of float32 partial products the product of `w` over `route` needs with these flags; 0 when it runs the
+ * fused kernels. Passes with few tokens per adapter segment (decode) split the input dimension into ranges whose
+ * float32 sums a second launch adds in order (the reference's split product); its size depends on the token count,
+ * the group's columns and inputs, not on device memory, so a caller can size its buffer once per shape. */
+size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                                 int32_t flags);
+
 /* y (tokens, w->out) bf16 = x W^T + each token's LoRA update, one rounding per output; x (tokens, k) bf16 rows
  * x_stride elements apart (k a multiple of 64, rows 16-byte aligned). last_out (requests, w->out) bf16 or NULL:
- * each request's last-token output row as well. */
+ * each request's last-token output row as well. workspace: the first factors (mlora_workspace_bytes);
+ * partials: mlora_int4_partials_bytes of float32 scratch (NULL when that is 0). */
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                       const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
-                      void* workspace, size_t workspace_bytes, int32_t flags, void* stream);
+                      void* workspace, size_t workspace_bytes, void* partials, size_t partials_bytes, int32_t flags,
+                      void* stream);
 
-/* mlora_int4_linear without its shrink launch: the base product with the LoRA second factor fused into its
- * epilogue, reading the first factors mid (tokens, rank_cap) that mlora_shrink wrote for the same route and x. */
+/* mlora_int4_linear without its shrink launch: the base product and the LoRA second factor, reading the first
+ * factors mid (tokens, rank_cap) that mlora_shrink wrote for the same route and x. */
 int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                            const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
-                           const uint16_t* mid, int32_t flags, void* stream);
+                           const uint16_t* mid, void* partials, size_t partials_bytes, int32_t flags, void* stream);
 
 /* In place: y (tokens, n_out) bf16 += each token's LoRA update (y read in float32, one rounding); x (tokens, k). */
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,

@@ -24,10 +24,10 @@ ERRORS = {EINVAL: "invalid argument (a null pointer, a bad size or shape)",
 
 ROUTE_BAD_ADAPTER = 1
 ROUTE_BAD_SEQLENS = 2
-FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_GEMV, FORCE_SHRINK_MFMA = 1, 2, 4, 8
+FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_GEMV, FORCE_SHRINK_MFMA, FORCE_BASE_SPLIT = 1, 2, 4, 8, 16
 
-EXPORTS = ("mlora_abi_version", "mlora_workspace_bytes", "mlora_route", "mlora_dequant", "mlora_shrink",
-           "mlora_int4_linear", "mlora_int4_base_expand", "mlora_lora_add")
+EXPORTS = ("mlora_abi_version", "mlora_workspace_bytes", "mlora_int4_partials_bytes", "mlora_route", "mlora_dequant",
+           "mlora_shrink", "mlora_int4_linear", "mlora_int4_base_expand", "mlora_lora_add")
 
 c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -85,10 +85,12 @@ def lib() -> ctypes.CDLL:
         h.mlora_shrink.argtypes = [P(Lora), P(Route), c_vp, c_i64, c_i32, c_vp, c_i32, c_vp]
         h.mlora_int4_linear.restype = c_i32
         h.mlora_int4_linear.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_vp,
-                                        ctypes.c_size_t, c_i32, c_vp]
+                                        ctypes.c_size_t, c_vp, ctypes.c_size_t, c_i32, c_vp]
         h.mlora_int4_base_expand.restype = c_i32
-        h.mlora_int4_base_expand.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i32,
-                                             c_vp]
+        h.mlora_int4_base_expand.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                             ctypes.c_size_t, c_i32, c_vp]
+        h.mlora_int4_partials_bytes.restype = ctypes.c_size_t
+        h.mlora_int4_partials_bytes.argtypes = [P(Int4), P(Lora), P(Route), c_i32]
         h.mlora_lora_add.restype = c_i32
         h.mlora_lora_add.argtypes = [P(Lora), P(Route), c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_vp,
                                      ctypes.c_size_t, c_i32, c_vp]

@@ -55,11 +55,73 @@ int check_rows(const void* p, int64_t stride, int32_t width) {
   return MLORA_OK;
 }
 
+// Long segments on average (prefill): at least 16 tokens per adapter segment.
+bool long_segments(const mlora_route_t* r, int32_t pool_rows) {
+  const int64_t segs = r->requests < pool_rows ? r->requests : pool_rows;
+  return r->tokens >= 16 * (segs > 0 ? segs : 1);
+}
+
 bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
   if (flags & MLORA_FORCE_SHRINK_MFMA) return true;
   if (flags & MLORA_FORCE_SHRINK_GEMV) return false;
-  const int64_t segs = r->requests < pool_rows ? r->requests : pool_rows;
-  return r->tokens >= 16 * (segs > 0 ? segs : 1);  // long segments on average: prefill
+  return long_segments(r, pool_rows);
+}
+
+enum class Base { gemv, fused, split };
+
+// The split product runs the 256 x 256 kernel (32-bit x offsets) and stages first factors of at most
+// MLORA_SPLIT_MAX_RANK stacked ranks.
+bool split_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride) {
+  return L->rank_cap <= MLORA_SPLIT_MAX_RANK && r->tokens * (x_stride > w->k ? x_stride : w->k) < ((int64_t)1 << 31);
+}
+
+// Which base kernels run; EUNSUPPORTED when the flags force one that cannot.
+int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
+            Base* out) {
+  if (flags & MLORA_FORCE_BASE_GEMV) {
+    if (r->tokens > 8) return MLORA_EUNSUPPORTED;
+    *out = Base::gemv;
+  } else if (flags & MLORA_FORCE_BASE_SPLIT) {
+    if (!split_fits(w, L, r, x_stride)) return MLORA_EUNSUPPORTED;
+    *out = Base::split;
+  } else if (flags & MLORA_FORCE_BASE_MFMA) {
+    *out = Base::fused;
+  } else if (r->tokens <= 8) {
+    *out = Base::gemv;
+  } else {
+    *out = !long_segments(r, L->pool_rows) && split_fits(w, L, r, x_stride) ? Base::split : Base::fused;
+  }
+  return MLORA_OK;
+}
+
+// Input ranges of a split product: the most (at most 8, each of at least 4 steps of 64 inputs, dividing the steps)
+// that keep the first launch within one workgroup per CU (256).
+int32_t split_ranges(const mlora_int4_t* w, int64_t tokens) {
+  const int64_t tiles = ((tokens + 255) / 256) * ((w->out + 255) / 256);
+  const int steps = w->k / 64;
+  int best = 1;
+  for (int s = 2; s <= 8; ++s)
+    if (steps % s == 0 && steps / s >= 4 && tiles * s <= 256) best = s;
+  return best;
+}
+
+size_t split_bytes(const mlora_int4_t* w, int64_t tokens) {
+  return ((size_t)split_ranges(w, tokens) * (size_t)tokens * (size_t)w->columns * 4 + 255) & ~(size_t)255;
+}
+
+// The base product (and the LoRA second factor) once mid holds the first factors.
+int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
+             int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
+             void* partials, size_t partials_bytes, Base base, hipStream_t s) {
+  if (base != Base::split)
+    return launch_base(w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, base == Base::gemv, s);
+  if (partials == nullptr || !aligned16(partials) || partials_bytes < split_bytes(w, r->tokens))
+    return MLORA_EWORKSPACE;
+  const int32_t ks = split_ranges(w, r->tokens);
+  float* part = static_cast<float*>(partials);
+  int rc = launch_base256(*w, *L, *r, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s);
+  if (rc) return rc;
+  return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
 }
 
 }  // namespace
@@ -110,9 +172,18 @@ int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uin
                        static_cast<hipStream_t>(stream));
 }
 
+size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                                 int32_t flags) {
+  if (check_int4(w) || check_route(route) || check_lora(lora, w->k, w->out) || route->tokens == 0) return 0;
+  Base base;
+  if (base_of(w, lora, route, w->k, flags, &base) || base != Base::split) return 0;
+  return split_bytes(w, route->tokens);
+}
+
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                       const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
-                      void* workspace, size_t workspace_bytes, int32_t flags, void* stream) {
+                      void* workspace, size_t workspace_bytes, void* partials, size_t partials_bytes, int32_t flags,
+                      void* stream) {
   int rc = check_int4(w);
   if (rc) return rc;
   if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
@@ -121,28 +192,30 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
   if (y == nullptr || y_stride < w->out) return MLORA_EINVAL;
   if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
   if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
-  const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
-  if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
+  Base base;
+  if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
+  if (base == Base::split && (partials == nullptr || partials_bytes < split_bytes(w, route->tokens)))
+    return MLORA_EWORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* mid = static_cast<uint16_t*>(workspace);
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, shrink_on_mfma(route, lora->pool_rows, flags), s)))
     return rc;
-  return launch_base(w, *lora, *route, x, x_stride, y, y_stride, last_out, w->out, mid, gemv, s);
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, s);
 }
 
 int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                            const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
-                           const uint16_t* mid, int32_t flags, void* stream) {
+                           const uint16_t* mid, void* partials, size_t partials_bytes, int32_t flags, void* stream) {
   int rc = check_int4(w);
   if (rc) return rc;
   if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, w->k))) return rc;
   if (y == nullptr || y_stride < w->out || mid == nullptr || !aligned16(mid)) return MLORA_EINVAL;
-  const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
-  if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
-  return launch_base(w, *lora, *route, x, x_stride, y, y_stride, last_out, w->out, mid, gemv,
-                     static_cast<hipStream_t>(stream));
+  Base base;
+  if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base,
+                  static_cast<hipStream_t>(stream));
 }
 
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
@@ -157,6 +230,7 @@ int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const u
   if (y == nullptr || y_stride < n_out) return MLORA_EINVAL;
   if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
   if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
+  if (flags & MLORA_FORCE_BASE_SPLIT) return MLORA_EUNSUPPORTED;  // no base product to split
   const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
   if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -280,7 +280,7 @@ int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_
                          y_stride, last_out, n_out, mid);
   } else if (w != nullptr && r.tokens >= kBigTileTokens && r.tokens * x_stride < ((int64_t)1 << 31)) {
     // (the 256 x 256 kernel addresses x rows with 32-bit element offsets)
-    return launch_base256(*w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, stream);
+    return launch_base256(*w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, nullptr, 1, stream);
   } else {
     const int m_tiles = (int)((r.tokens + kBM - 1) / kBM);
     const int n_tiles = (n_out + kBN - 1) / kBN;

@@ -74,10 +74,14 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
-                                                               const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec) {
+                                                               const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec,
+                                                               float* __restrict__ part, int32_t ksplit) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
-  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  // Block b -> (K range ks, row tile mt, column tile nt), column tiles innermost: the blocks that share x rows (one
+  // row tile and K range) are consecutive and so run on one XCD.
+  const int b = xcd_tile(blockIdx.x, gridDim.x);
+  const int t = b % (gridDim.x / ksplit), ks = b / (gridDim.x / ksplit);
   const int mt = t / n_tiles, nt = t - mt * n_tiles;
   const int64_t T = r.tokens;
   const int64_t p0 = (int64_t)mt * kTM;
@@ -85,9 +89,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
   // Loads go through buffer resources: the per-lane byte offsets below stay fixed for the whole K loop and the K
   // position is a wave-uniform scalar offset, so no 64-bit addresses are kept in registers. The resources' sizes
-  // are the arrays' sizes (the host keeps tokens x x_stride below 2^31 elements).
+  // are the arrays' sizes, except for x, gathered row by row, whose resource spans the whole 32-bit range (the host
+  // keeps tokens x x_stride below 2^31 elements, so every byte offset fits 32 bits).
   const __amdgpu_buffer_rsrc_t xres =
-      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, 0x7fffffff, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)0xFFFFFFFFu, 0x00020000);
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)w.words, (short)0, (int)((int64_t)(w.k / 8) * w.columns * 4), 0x00020000);
   const int64_t groups = w.k / w.group;
@@ -206,11 +211,12 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // start of step i - 1). Every load is unconditional (past the last step it re-reads the last one into a buffer or
   // set that is never used), so the number of loads in flight at each wait is the same on every path:
   // after x(i + 1) come w(i), x(i + 2) and w(i + 1).
-  const int nk = w.k / kTK;
+  const int nk = w.k / kTK / ksplit;  // this block's K steps, from step ks * nk
+  const int kbase = ks * nk * kTK;
   WStage s0, s1;
-  dma_x(g_x0, 0);
-  fetch_w(s0, 0);
-  dma_x(g_x1, min(1, nk - 1) * kTK);
+  dma_x(g_x0, kbase);
+  fetch_w(s0, kbase);
+  dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
   MLORA_WAIT_VM(kWLoads + kXLoads);  // x(0) has landed
   lds_sync();
   auto run = [&](auto xb, auto wb, int i) {
@@ -219,8 +225,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;  // buffer (i + 2) % 3
     WStage& cur = WB == 0 ? s0 : s1;
     WStage& nxt = WB == 0 ? s1 : s0;
-    dma_x(xf, min(i + 2, nk - 1) * kTK);
-    fetch_w(nxt, min(i + 1, nk - 1) * kTK);
+    dma_x(xf, kbase + min(i + 2, nk - 1) * kTK);
+    fetch_w(nxt, kbase + min(i + 1, nk - 1) * kTK);
     step(xs, cur);
     MLORA_WAIT_VM(kWLoads + kXLoads + kWLoads);  // x(i + 1) has landed
     lds_sync();
@@ -243,6 +249,27 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   }
   MLORA_WAIT_VM(0);
   lds_sync();
+
+  if (part != nullptr) {
+    // Split product: this K range's float32 sums to part[ks][p][c] (sorted rows, `columns` columns per row); the
+    // second launch adds the ranges in order, the LoRA term and rounds. Lane l holds four consecutive columns.
+    float* pk = part + (int64_t)ks * T * w.columns;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int64_t p = p0 + wm * 128 + mb * 32 + (lane & 31);
+      if (p >= T) continue;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = n0 + wn * 64 + nb * 32 + g * 8 + (lane >> 5) * 4;
+          if (c >= w.columns) continue;
+          *reinterpret_cast<float4*>(pk + p * w.columns + c) =
+              make_float4(acc[mb][nb][4 * g], acc[mb][nb][4 * g + 1], acc[mb][nb][4 * g + 2], acc[mb][nb][4 * g + 3]);
+        }
+    }
+    return;
+  }
 
   // LoRA second factor. The tile's rows of the first factor (sorted order, ranks rc .. rc + 63 of matrix j) are
   // staged in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come
@@ -384,15 +411,15 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, hipStream_t stream) {
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
   const int m_tiles = (int)((r.tokens + kTM - 1) / kTM);
   const int n_tiles = (n_out + kTN - 1) / kTN;
-  const int64_t blocks = (int64_t)m_tiles * n_tiles;
+  const int64_t blocks = (int64_t)m_tiles * n_tiles * ksplit;
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);
   hipLaunchKernelGGL(base_mfma256_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, w, L, r, x, x_stride, y,
-                     y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec);
+                     y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

@@ -123,15 +123,23 @@ __device__ __forceinline__ int matrix_of(const mlora_lora_t& L, int c) {
 
 }  // namespace mlora
 
+// The split product's second launch stages its rows' first factors in LDS: at most this stacked rank.
+#define MLORA_SPLIT_MAX_RANK 512
+
 // Launchers (one per kernel family), defined in their .hip files; each returns MLORA_OK or MLORA_ELAUNCH.
 int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const mlora_route_t& r, int32_t pool_rows,
                  hipStream_t stream);
 int launch_dequant(const mlora_int4_t& w, uint16_t* out, hipStream_t stream);
 int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x, int64_t x_stride, int32_t k,
                   uint16_t* mid, bool mfma, hipStream_t stream);
+// 256 x 256 tiles; with part != nullptr the split mode: ksplit input ranges, float32 sums to part, nothing else.
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, hipStream_t stream);
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream);
+// The second launch of a split product: partial sums in order + LoRA term, rounded once.
+int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
+                  const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+                  hipStream_t stream);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

@@ -176,6 +176,18 @@ class Workspace:
         self.status = torch.zeros(1, **i32)
         self._routed: tuple | None = None
         self._route_abi: _lib.Route | None = None
+        self._part: torch.Tensor | None = None
+
+    def partials(self, nbytes: int) -> tuple[int, int]:
+        """(pointer, bytes) of device scratch for a split product's float32 partial sums, at least nbytes (0: none
+        needed). Grown when a larger product comes and kept, like the reference's Workspace.P
+        (engine/int4_kernels.py:150-166)."""
+        if nbytes == 0:
+            return 0, 0
+        if self._part is None or self._part.numel() < nbytes:
+            self._part = None
+            self._part = torch.empty(nbytes, dtype=torch.uint8, device=self.mid.device)
+        return self._part.data_ptr(), self._part.numel()
 
     def route(self, adp: torch.Tensor, pool_rows: int, tokens: int | None = None,
               cu_seqlens: torch.Tensor | None = None) -> _lib.Route:

@@ -2,10 +2,12 @@
 
 Mirrors the reference's engine/int4_kernels.py:132-177 (int4_product(lin, x, ws, adp, tiles=None)): same arguments,
 a new bf16 (tokens, lin.out) result, ValueError before any allocation or launch for a group without INT4 weights, an
-input that is not a contiguous bf16 (tokens, lin.k) tensor, or a pass too large for the kernels. Two launches on
-the current stream (the LoRA first factor, then the base product with the second factor fused into its epilogue,
-rounded once), plus the routing launch when the workspace has not routed `adp` yet. Deterministic: no atomic
-additions, every sum in a fixed order."""
+input that is not a contiguous bf16 (tokens, lin.k) tensor, or a pass too large for the kernels. On the current
+stream: the LoRA first factor, then either the base product with the second factor fused into its epilogue (one
+launch, rounded once) or, for passes with few tokens per adapter (decode), the reference's split product: float32
+partial products over ranges of the input dimension, then one epilogue launch per (adapter segment, 256 columns)
+that adds them in order with the LoRA term and rounds once. Plus the routing launch when the workspace has not
+routed `adp` yet. Deterministic: no atomic additions, every sum in a fixed order."""
 
 from __future__ import annotations
 
@@ -39,10 +41,13 @@ def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, ti
     r = ws.routed(adp, lin.pool.shape[0], m)
     y = torch.empty(m, lin.out, device=x.device, dtype=DT)
     h = _lib.lib()
+    flags = 0 if tiles is None else tiles.flags()
+    w, lora = packed.abi(), lin.lora_abi()
+    part, part_bytes = ws.partials(h.mlora_int4_partials_bytes(w, lora, r, flags))
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    _lib.check(h.mlora_int4_linear(packed.abi(), lin.lora_abi(), r, x.data_ptr(), x.stride(0), y.data_ptr(),
-                                   y.stride(0), 0 if last_out is None else last_out.data_ptr(), ws.mid.data_ptr(),
-                                   ws.mid.numel() * 2, 0 if tiles is None else tiles.flags(), stream),
+    _lib.check(h.mlora_int4_linear(w, lora, r, x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0),
+                                   0 if last_out is None else last_out.data_ptr(), ws.mid.data_ptr(),
+                                   ws.mid.numel() * 2, part, part_bytes, flags, stream),
                "mlora_int4_linear")
     return y
 
@@ -63,8 +68,8 @@ def shrink(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, mfma: bo
 
 def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: torch.Tensor,
                 tiles: Int4Tiles | None = None, last_out: torch.Tensor | None = None) -> torch.Tensor:
-    """The second launch of int4_product alone, into a given y: the base product with the LoRA second factor fused,
-    reading the first factors the last shrink (or int4_product) of the same x and adp left in the workspace."""
+    """int4_product without its first launch, into a given y: the base product and the LoRA second factor, reading
+    the first factors the last shrink (or int4_product) of the same x and adp left in the workspace."""
     packed = lin.int4
     if packed is None:
         raise ValueError(f"{', '.join(lin.names)}: no INT4 weights")
@@ -74,9 +79,12 @@ def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: 
         raise ValueError(f"y must be bfloat16 ({m}, {lin.out}) with contiguous rows")
     r = ws.routed(adp, lin.pool.shape[0], m)
     h = _lib.lib()
+    flags = 0 if tiles is None else tiles.flags()
+    w, lora = packed.abi(), lin.lora_abi()
+    part, part_bytes = ws.partials(h.mlora_int4_partials_bytes(w, lora, r, flags))
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    _lib.check(h.mlora_int4_base_expand(packed.abi(), lin.lora_abi(), r, x.data_ptr(), x.stride(0), y.data_ptr(),
-                                        y.stride(0), 0 if last_out is None else last_out.data_ptr(),
-                                        ws.mid.data_ptr(), 0 if tiles is None else tiles.flags(), stream),
+    _lib.check(h.mlora_int4_base_expand(w, lora, r, x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0),
+                                        0 if last_out is None else last_out.data_ptr(), ws.mid.data_ptr(), part,
+                                        part_bytes, flags, stream),
                "mlora_int4_base_expand")
     return y

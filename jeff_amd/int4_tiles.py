@@ -3,7 +3,9 @@ without a GPU). The reference chooses Triton tiles here (engine/int4_tiles.py:57
 kernel family instead, and the tiles inside each family are fixed for gfx950.
 
 - base: "gemv" (at most GEMV_MAX_TOKENS tokens: one pass over the weights, every token dotted with each dequantised
-  word) or "mfma" (32x32x16 bf16 MFMA tiles of 128 tokens x 128 columns).
+  word), "mfma" (32x32x16 bf16 MFMA tiles, the LoRA second factor fused into the epilogue) or "split" (few tokens
+  per adapter segment: MFMA tiles over ranges of the input dimension into float32 partials, then one epilogue
+  workgroup per adapter segment and 256 columns).
 - shrink (the LoRA first factor): "gemv" when segments are short on average (decode: one workgroup streams 16 ranks
   of one adapter's A) or "mfma" when they are long (prefill: 64-token tiles on MFMA).
 The library makes the same choice itself when no flag forces one (api.hip, shrink_on_mfma)."""
@@ -16,7 +18,7 @@ from jeff_amd import _lib
 
 GEMV_MAX_TOKENS = 8
 SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT = 16
-BASES = ("gemv", "mfma")
+BASES = ("gemv", "mfma", "split")
 SHRINKS = ("gemv", "mfma")
 
 
@@ -26,7 +28,7 @@ class Int4Tiles:
     shrink: str
 
     def flags(self) -> int:
-        f = _lib.FORCE_BASE_GEMV if self.base == "gemv" else _lib.FORCE_BASE_MFMA
+        f = {"gemv": _lib.FORCE_BASE_GEMV, "mfma": _lib.FORCE_BASE_MFMA, "split": _lib.FORCE_BASE_SPLIT}[self.base]
         return f | (_lib.FORCE_SHRINK_GEMV if self.shrink == "gemv" else _lib.FORCE_SHRINK_MFMA)
 
 
@@ -37,8 +39,8 @@ def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = No
     if columns <= 0 or columns % 64 or inputs <= 0 or inputs % 64 or tokens <= 0:
         raise ValueError(f"The INT4 kernels need columns and inputs that are positive multiples of 64 and at least one "
                          f"token; got {columns} columns, {inputs} inputs, {tokens} tokens")
-    base = "gemv" if tokens <= GEMV_MAX_TOKENS else "mfma"
     requests = tokens if requests is None else requests
     segs = max(1, min(requests, pool_rows if pool_rows is not None else requests))
-    shrink = "mfma" if tokens >= SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT * segs else "gemv"
-    return Int4Tiles(base, shrink)
+    long_segments = tokens >= SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT * segs
+    base = "gemv" if tokens <= GEMV_MAX_TOKENS else "mfma" if long_segments else "split"
+    return Int4Tiles(base, "mfma" if long_segments else "gemv")
