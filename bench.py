@@ -36,11 +36,45 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="bound on the CPU baseline's timed work")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches of the dominant kernel timed (0: auto)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of COPY_BYTES five times (the scale of the HBM byte counters)")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+TRAFFIC_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def copy_calibration() -> int:
+    """Five copies of COPY_BYTES between two device buffers (torch's copy kernel): a profile of this run reads
+    FETCH_SIZE and WRITE_SIZE for a known number of bytes moved, the factor that turns those counters into bytes."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 5}))
+    return 0
+
+
+def measured_traffic(workload: str) -> float | None:
+    """HBM bytes per launch of the dominant kernel from the committed counter profile of this workload
+    (profiles/traffic_<workload>.txt, a line `bytes_per_launch=<N>`), or None when there is none."""
+    path = os.path.join(TRAFFIC_DIR, f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("bytes_per_launch="):
+                return float(line.split("=", 1)[1])
+    return None
 
 
 def main() -> int:
     args = parse()
+    if args.copy_calibration:
+        return copy_calibration()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
@@ -51,6 +85,7 @@ def main() -> int:
     from jeff_amd import workloads
     from jeff_amd.fast_path import DT, Workspace
     from jeff_amd.int4_kernels import base_expand, int4_product, shrink
+    from jeff_amd.int4_tiles import int4_tiles
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -101,8 +136,9 @@ def main() -> int:
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     tokens_per_s = w.tokens / (ms_per_step / 1e3)
 
-    # the dominant kernel alone: the base product with the fused expand of the largest group of layer 0, timed with
-    # HIP events on the stream it runs on (the first factors it reads are computed once beforehand)
+    # the dominant kernel alone: the base product and the LoRA second factor of the largest group of layer 0 (one
+    # launch of the fused 256-tile kernel for prefill; for decode the split product's two launches), timed with HIP
+    # events on the stream it runs on (the first factors it reads are computed once beforehand)
     label = DOMINANT[args.workload]
     lin = w.layers[0][label]
     x = xs[(0, label)]
@@ -137,16 +173,22 @@ def main() -> int:
         launch_ms.append(e0.elapsed_time(e1) / reps)
     kms = statistics.median(launch_ms)
     mfma_bound = args.workload.startswith("prefill")
+    traffic = measured_traffic(args.workload)
     if mfma_bound:
         achieved = kflops / (kms / 1e3)
         roof = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / PEAK_BF16, "traffic": None}
+                "frac": achieved / PEAK_BF16, "traffic": traffic}
     else:
         achieved = kbytes / (kms / 1e3)
         roof = {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": achieved / PEAK_HBM, "traffic": None}
-    roof.update({"kernel": "base_mfma_kernel<true> (INT4 base + fused LoRA expand)", "group": f"layer0.{label}",
-                 "launch_ms": kms, "flops_per_launch": kflops, "bytes_per_launch": kbytes})
+                "frac": achieved / PEAK_HBM, "traffic": traffic}
+    tiles = int4_tiles(lin.int4.columns, lin.k, w.tokens, w.requests, pool_rows)
+    kernel = {"mfma": "base_mfma256_kernel (INT4 base + fused LoRA expand)" if w.tokens >= 1024 else
+              "base_mfma_kernel<true> (INT4 base + fused LoRA expand)",
+              "split": "base_mfma256_kernel, split mode + finish_kernel (INT4 base + LoRA expand, 2 launches)",
+              "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[tiles.base]
+    roof.update({"kernel": kernel, "group": f"layer0.{label}", "launch_ms": kms, "flops_per_launch": kflops,
+                 "bytes_per_launch": kbytes})
     step_flops = workloads.flops_per_token(w) * w.tokens
     step_bytes = workloads.hbm_bytes(w)
     step_roof = {"mfma_frac": step_flops / (ms_per_step / 1e3) / PEAK_BF16,
