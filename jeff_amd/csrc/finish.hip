@@ -21,9 +21,10 @@ constexpr int kFinThreads = 256;  // one output column per thread
 constexpr int kFinRows = 8;       // sorted rows per pass
 constexpr int kFinRanks = 64;     // sB ranks staged per pass
 constexpr int kFinPitch = kFinRanks + 8;
+constexpr int kRegRows = 4;     // sorted rows per pass of the register form (decode segments hold a few)
 constexpr int kMaxSplit = 8;     // input ranges of a split product (the host picks at most this many)
 
-__global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlora_route_t r,
+__global__ __launch_bounds__(kFinThreads) void finish_lds_kernel(mlora_lora_t L, mlora_route_t r,
                                                             const float* __restrict__ part, int32_t ksplit,
                                                             int32_t ld, const uint16_t* __restrict__ mid,
                                                             uint16_t* __restrict__ y, int64_t y_stride,
@@ -134,6 +135,155 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlo
   }
 }
 
+// Sum of v over the CPC consecutive lanes of a column group (CPC = 1, 2, 4 or 8), every lane of the group ending with
+// the same bits: DPP lane moves (xor 1, xor 2 within quads, then the mirrored quad of the 8-lane half row), each
+// step adding two equal-order partial sums.
+template <int CPC>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (CPC >= 2)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  if constexpr (CPC >= 4)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  if constexpr (CPC >= 8)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
+// One (segment, 256 columns of matrix j) of a matrix whose sB rows hold CPC * 8 ranks (cap_j = 8, 16, 32 or 64).
+// Thread t takes 16-byte chunk t % CPC of the rows of columns t / CPC + (256 / CPC) i, i < CPC: consecutive threads
+// read consecutive 16 bytes of the contiguous sB block. Per pass of kRegRows rows:
+//  - every thread sums four columns of one row's base partials over the input ranges (coalesced 16-byte loads, all
+//    ranges in flight) into LDS;
+//  - each lane dots its sB chunk with the same ranks of every row's first factor, the CPC lanes of a column add
+//    their partial sums (group_sum), and lane t % CPC == row % CPC adds the base sum and rounds into an LDS tile;
+//  - the tile's rows are written with coalesced 8-byte stores.
+template <int CPC>
+__device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlora_route_t& r,
+                                               const float* __restrict__ part, int32_t ksplit, int32_t ld,
+                                               const uint16_t* __restrict__ mid, uint16_t* __restrict__ y,
+                                               int64_t y_stride, uint16_t* __restrict__ last_out, int32_t n_out,
+                                               int64_t sb, int64_t se, int a, int j, int oj, int c0, int ncols,
+                                               bool vec, float* __restrict__ base_lds, uint16_t* __restrict__ out_lds) {
+  const int tid = threadIdx.x;
+  const int ch = tid % CPC, cl = tid / CPC;
+  const int capj = L.cap[j];
+  const int rk = a != 0 ? live_rank(L, a, j) : 0;
+  const int rho = rank_offset(L, j);
+  const int rc = L.rank_cap;
+  const bool chunk_live = 8 * ch < rk;
+  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * capj;
+  const int64_t T = r.tokens;
+  uint4 bv[CPC];
+#pragma unroll
+  for (int i = 0; i < CPC; ++i) {
+    const int col = cl + (kFinThreads / CPC) * i;
+    bv[i] = (chunk_live && col < ncols)
+                ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * capj + 8 * ch), rk - 8 * ch)
+                : make_uint4(0, 0, 0, 0);
+  }
+  // the thread's four columns of one row for the base sums and the stores
+  const int srow = tid / (kFinThreads / 4), scol = 4 * (tid % (kFinThreads / 4));
+  for (int64_t p0 = sb; p0 < se; p0 += kRegRows) {
+    const int rows = (int)min((int64_t)kRegRows, se - p0);
+    // base partial sums, in range order
+    float4 pv[kMaxSplit];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp)
+      pv[sp] = (sp < ksplit && srow < rows && scol < ncols)
+                   ? *reinterpret_cast<const float4*>(part + ((int64_t)sp * T + p0 + srow) * ld + oj + c0 + scol)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // first factors of the rows, this lane's 8 ranks; ranks past the live rank masked to zero (they are not written)
+    uint4 mv[kRegRows];
+#pragma unroll
+    for (int rr = 0; rr < kRegRows; ++rr)
+      mv[rr] = (chunk_live && rr < rows)
+                   ? keep_first(*reinterpret_cast<const uint4*>(mid + (p0 + rr) * rc + rho + 8 * ch), rk - 8 * ch)
+                   : make_uint4(0, 0, 0, 0);
+    float4 bsum = pv[0];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplit; ++sp) {
+      bsum.x += pv[sp].x;
+      bsum.y += pv[sp].y;
+      bsum.z += pv[sp].z;
+      bsum.w += pv[sp].w;
+    }
+    __syncthreads();  // the previous pass is done with both LDS tiles
+    *reinterpret_cast<float4*>(&base_lds[srow * kFinThreads + scol]) = bsum;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPC; ++i) {
+      const int col = cl + (kFinThreads / CPC) * i;
+#pragma unroll
+      for (int rr = 0; rr < kRegRows; ++rr) {
+        if (rr >= rows) break;
+        const float lora = group_sum<CPC>(dot8(bv[i], mv[rr], 0.0f));
+        if (rr % CPC == ch) out_lds[rr * kFinThreads + col] = f32_to_bf16(base_lds[rr * kFinThreads + col] + lora);
+      }
+    }
+    __syncthreads();
+    if (srow < rows && scol < ncols) {
+      const int64_t p = p0 + srow;
+      const int c = oj + c0 + scol;
+      const uint2 v = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
+      const int q = last_out != nullptr ? r.last_of[p] : -1;
+      uint16_t* yrow = y + (int64_t)r.tok_perm[p] * y_stride;
+      if (vec && scol + 4 <= ncols) {
+        *reinterpret_cast<uint2*>(yrow + c) = v;
+        if (q >= 0) *reinterpret_cast<uint2*>(last_out + (int64_t)q * n_out + c) = v;
+      } else {
+        const uint16_t h[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
+        for (int e = 0; e < 4 && scol + e < ncols; ++e) {
+          yrow[c + e] = h[e];
+          if (q >= 0) last_out[(int64_t)q * n_out + c + e] = h[e];
+        }
+      }
+    }
+  }
+}
+
+// The register form of the split product's second launch: every matrix of the group has cap_j in {8, 16, 32, 64}.
+__global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlora_route_t r,
+                                                            const float* __restrict__ part, int32_t ksplit,
+                                                            int32_t ld, const uint16_t* __restrict__ mid,
+                                                            uint16_t* __restrict__ y, int64_t y_stride,
+                                                            uint16_t* __restrict__ last_out, int32_t n_out,
+                                                            int32_t vec) {
+  __shared__ __attribute__((aligned(16))) float base_lds[kRegRows * kFinThreads];
+  __shared__ __attribute__((aligned(16))) uint16_t out_lds[kRegRows * kFinThreads];
+  const int s = blockIdx.y;
+  if (s >= *r.num_segs) return;
+  const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+  if (se <= sb) return;
+  int j = 0, cb = blockIdx.x, oj = 0;
+  while (j + 1 < L.n_mats && cb >= (L.cols[j] + kFinThreads - 1) / kFinThreads) {
+    cb -= (L.cols[j] + kFinThreads - 1) / kFinThreads;
+    oj += L.cols[j];
+    ++j;
+  }
+  const int c0 = cb * kFinThreads;
+  const int ncols = min(kFinThreads, L.cols[j] - c0);
+  if (ncols <= 0) return;
+  const int a = r.seg_adapter[s];
+  switch (L.cap[j]) {
+    case 64:
+      finish_columns<8>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+                        vec != 0, base_lds, out_lds);
+      break;
+    case 32:
+      finish_columns<4>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+                        vec != 0, base_lds, out_lds);
+      break;
+    case 16:
+      finish_columns<2>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+                        vec != 0, base_lds, out_lds);
+      break;
+    default:  // 8, or 0 (no adapter on this matrix: the base partial sums only)
+      finish_columns<1>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+                        vec != 0, base_lds, out_lds);
+      break;
+  }
+}
+
 }  // namespace
 
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
@@ -141,9 +291,23 @@ int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* pa
                   hipStream_t stream) {
   if (r.tokens == 0 || n_out == 0 || r.max_segs == 0) return MLORA_OK;
   int blocks = 0;
-  for (int j = 0; j < L.n_mats; ++j) blocks += (L.cols[j] + kFinThreads - 1) / kFinThreads;
+  // the register form: every cap_j in {0, 8, 16, 32, 64} and every matrix a multiple of four columns (its partial
+  // sums are read four columns at a time)
+  bool registers = true;
+  for (int j = 0; j < L.n_mats; ++j) {
+    blocks += (L.cols[j] + kFinThreads - 1) / kFinThreads;
+    const int c = L.cap[j];
+    registers = registers && (c == 0 || c == 8 || c == 16 || c == 32 || c == 64) && L.cols[j] % 4 == 0;
+  }
   const dim3 grid((unsigned)blocks, (unsigned)r.max_segs);
-  hipLaunchKernelGGL(finish_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y, y_stride,
-                     last_out, n_out);
+  // 8-byte stores of four columns: 8-byte aligned output rows
+  const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
+                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0));
+  if (registers)
+    hipLaunchKernelGGL(finish_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y, y_stride,
+                       last_out, n_out, (int32_t)vec);
+  else
+    hipLaunchKernelGGL(finish_lds_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
+                       y_stride, last_out, n_out);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

@@ -4,8 +4,9 @@
 // (engine/fast_path.py:159-177,196; engine/int4_kernels.py:67-82,120). Two kernels, chosen by segment length:
 //  - shrink_gemv: few tokens per adapter (decode). One workgroup per (segment, matrix, 16 ranks) streams those 16
 //    rows of A once, coalesced, and reduces across the workgroup in a fixed order. Memory-bound on A.
-//  - shrink_mfma: long segments (prefill). One workgroup per 64 sorted positions stages x through LDS and runs
-//    32x32x16 bf16 MFMAs against each overlapping segment's A.
+//  - shrink_mfma: long segments (prefill). One workgroup per 32 sorted positions; its waves split the inputs, stream
+//    the x rows through per-wave LDS rings and A into registers one chunk ahead, and add their partial sums in a
+//    fixed order.
 #include "mlora_common.h"
 
 namespace {
@@ -81,11 +82,6 @@ __global__ __launch_bounds__(kGemvThreads) void shrink_gemv_kernel(mlora_lora_t 
   }
 }
 
-constexpr int kSM = 64;         // sorted positions per workgroup: 2 row blocks of 32
-constexpr int kSK = 64;         // inputs per step
-constexpr int kSLd = kSK + 8;   // LDS row stride in bf16 (144 bytes: 16-byte reads of 32 rows hit distinct banks)
-constexpr int kMaxBlocks = 8;   // 32-rank blocks per pass (256 ranks)
-
 // The (matrix, 32-rank block) of block index b of an adapter whose live ranks are rk[].
 __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int& j, int& kb) {
   j = 0;
@@ -96,108 +92,148 @@ __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int
   kb = b;
 }
 
-// One workgroup per 64 sorted positions and every segment crossing them: x rows and the segment's A rows are staged
-// through double-buffered LDS (the next step's loads in flight while the MFMAs run, one barrier per step); waves
-// (row block rb, half) take the rank blocks of their half.
-__global__ __launch_bounds__(256) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
-                                                         const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
-                                                         uint16_t* __restrict__ mid) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kSM * kSLd];
-  __shared__ __attribute__((aligned(16))) uint16_t as[2][kMaxBlocks * 32 * kSLd];
+constexpr int kSRows = 32;    // sorted rows per workgroup
+constexpr int kSWaves = 8;    // waves per workgroup, each a contiguous share of the inputs
+constexpr int kSBlocks = 2;   // 32-rank blocks per pass
+constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
+constexpr int kSLoads = 4 + 4 * kSBlocks;  // memory instructions per chunk and lane: x rows to LDS, then A
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Per-wave rings of two x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
+__shared__ __attribute__((aligned(16))) uint16_t s_ring0[kSWaves * kSRows * kSChunk];
+__shared__ __attribute__((aligned(16))) uint16_t s_ring1[kSWaves * kSRows * kSChunk];
+
+#define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+
+// Long segments (prefill): one workgroup per 32 sorted rows; its 8 waves split the input dimension into chunks of
+// 64. A wave streams its chunks of the 32 x rows (gathered through the sorted order) into its own LDS ring with
+// buffer loads that cover whole 128-byte rows, one chunk ahead, and loads the matching A operands into registers
+// one chunk ahead; one 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's
+// accumulators hold four consecutive ranks of one token. The eight partial sums are added in wave order in LDS
+// and rounded once. Rows outside the segment read zero x operands.
+__global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
+                                                                  const uint16_t* __restrict__ x, int64_t x_stride,
+                                                                  int32_t k, uint16_t* __restrict__ mid) {
   const int64_t T = r.tokens;
-  const int64_t p0 = (int64_t)blockIdx.x * kSM;
+  const int64_t p0 = (int64_t)blockIdx.x * kSRows;
   if (p0 >= T) return;
-  const int nseg = *r.num_segs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rb = wave & 1, half = wave >> 1;
-  const int64_t tile_end = min(p0 + kSM, T);
-  const int srow = tid >> 2, scol = (tid & 3) * 16;  // x staging: 16 inputs of one row
-  const int arow = tid >> 3, acol = (tid & 7) * 8;   // A staging: 8 inputs of one rank row per block
-  const int64_t sp = p0 + srow;
-  const int nk = k / kSK;
-  for (int s = segment_of(r.seg_start, nseg, p0); s < nseg && r.seg_start[s] < tile_end; ++s) {
-    const int64_t sb = max((int64_t)r.seg_start[s], p0), se = min((int64_t)r.seg_start[s + 1], tile_end);
-    if (se <= sb) continue;
+  const int64_t prow = p0 + (lane & 31);
+  const int nch = k / kSChunk;
+  const int c0 = (wave * nch) / kSWaves, c1 = ((wave + 1) * nch) / kSWaves;  // this wave's chunks
+  // x staging: instruction i fills rows 8 i .. 8 i + 7 of the wave's ring slot; lane l writes 16-byte slot l & 7 of
+  // row 8 i + (l >> 3), which holds logical chunk (l & 7) ^ (row & 7)
+  const uint16_t* xsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    const int64_t p = p0 + row;
+    xsrc[i] = x + (int64_t)r.tok_perm[p < T ? p : p0] * x_stride + 8 * ((lane & 7) ^ (row & 7));
+  }
+  uint16_t* const ring0 = s_ring0 + wave * kSRows * kSChunk;
+  uint16_t* const ring1 = s_ring1 + wave * kSRows * kSChunk;
+  const int orow = lane & 31;  // the operand row of this lane
+  const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kSRows, T) - 1];
+  for (int s = s_lo; s <= s_hi; ++s) {
     const int a = r.seg_adapter[s];
+    if (a == 0) continue;  // the base row: no first factor is read
+    const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+    const bool rin = prow >= sb && prow < se;
     int rk[MLORA_MAX_MATS];
     int nblk = 0;
     for (int j = 0; j < L.n_mats; ++j) {
       rk[j] = live_rank(L, a, j);
       nblk += (rk[j] + 31) >> 5;
     }
-    if (nblk == 0) continue;
-    const uint16_t* xsrc = (sp >= sb && sp < se) ? x + (int64_t)r.tok_perm[sp] * x_stride + scol : nullptr;
-    const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a;
-    for (int b0 = 0; b0 < nblk; b0 += kMaxBlocks) {
-      const int nbp = min(kMaxBlocks, nblk - b0);
-      const uint16_t* asrc[kMaxBlocks];
+    const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a + 8 * (lane >> 5);
+    for (int b0 = 0; b0 < nblk; b0 += kSBlocks) {
+      const uint16_t* asrc[kSBlocks];
+      bool aok[kSBlocks];
 #pragma unroll
-      for (int bi = 0; bi < kMaxBlocks; ++bi) {
-        asrc[bi] = nullptr;
-        if (bi < nbp) {
-          int j, kb;
-          rank_block(rk, L.n_mats, b0 + bi, j, kb);
-          const int n = kb * 32 + arow;
-          if (n < rk[j]) asrc[bi] = Abase + (int64_t)(rank_offset(L, j) + n) * k + acol;
-        }
+      for (int bi = 0; bi < kSBlocks; ++bi) {
+        int j = 0, kb = 0;
+        rank_block(rk, L.n_mats, min(b0 + bi, nblk - 1), j, kb);
+        const int n = kb * 32 + (lane & 31);
+        aok[bi] = b0 + bi < nblk && n < rk[j];
+        asrc[bi] = Abase + (int64_t)(rank_offset(L, j) + (aok[bi] ? n : 0)) * k;
       }
-      uint4 xv[2], av[kMaxBlocks];
-      auto fetch = [&](int kc) {
-        xv[0] = xv[1] = make_uint4(0, 0, 0, 0);
-        if (xsrc != nullptr) {
-          xv[0] = *reinterpret_cast<const uint4*>(xsrc + kc);
-          xv[1] = *reinterpret_cast<const uint4*>(xsrc + kc + 8);
-        }
+      f32x16_t acc[kSBlocks];
 #pragma unroll
-        for (int bi = 0; bi < kMaxBlocks; ++bi)
-          av[bi] = asrc[bi] != nullptr ? *reinterpret_cast<const uint4*>(asrc[bi] + kc) : make_uint4(0, 0, 0, 0);
-      };
-      auto stage = [&](int buf) {
-        *reinterpret_cast<uint4*>(&xs[buf][srow * kSLd + scol]) = xv[0];
-        *reinterpret_cast<uint4*>(&xs[buf][srow * kSLd + scol + 8]) = xv[1];
+      for (int bi = 0; bi < kSBlocks; ++bi) acc[bi] = f32x16_t{};
+      // rows outside the segment and rank rows past the live rank multiply as zeros (bit masks, not branches)
+      const uint32_t xmask = rin ? 0xFFFFFFFFu : 0u;
+      uint32_t amask[kSBlocks];
 #pragma unroll
-        for (int bi = 0; bi < kMaxBlocks; ++bi)
-          if (bi < nbp) *reinterpret_cast<uint4*>(&as[buf][(bi * 32 + arow) * kSLd + acol]) = av[bi];
-      };
-      f32x16_t acc[kMaxBlocks / 2];
+      for (int bi = 0; bi < kSBlocks; ++bi) amask[bi] = aok[bi] ? 0xFFFFFFFFu : 0u;
+      if (c1 > c0) {
+        uint4 aq0[4][kSBlocks], aq1[4][kSBlocks];
+        // one chunk's loads: its x rows into a ring slot, its A operands into registers; every load is unconditional
+        // (chunks past the wave's range re-read its last one), so the counts the waits rely on hold on every path
+        auto issue = [&](uint16_t* slot, uint4 (&aq)[4][kSBlocks], int c) {
+          const int kc = min(c, c1 - 1) * kSChunk;
 #pragma unroll
-      for (int m = 0; m < kMaxBlocks / 2; ++m) acc[m] = f32x16_t{};
-      fetch(0);
-      stage(0);
-      if (nk > 1) fetch(kSK);
-      __syncthreads();
-      for (int it = 0; it < nk; ++it) {
-        const int cur = it & 1;
+          for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + kc, (lds_void*)(slot + i * 8 * kSChunk), 16, 0, 0);
 #pragma unroll
-        for (int k16 = 0; k16 < kSK / 16; ++k16) {
-          const int kk = k16 * 16 + (lane >> 5) * 8;
-          const uint4 av16 = *reinterpret_cast<const uint4*>(&xs[cur][(rb * 32 + (lane & 31)) * kSLd + kk]);
+          for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int m = 0; m < kMaxBlocks / 2; ++m) {
-            const int bi = half + 2 * m;
-            if (bi < nbp) {
-              const uint4 bv = *reinterpret_cast<const uint4*>(&as[cur][(bi * 32 + (lane & 31)) * kSLd + kk]);
-              acc[m] = mfma32(av16, bv, acc[m]);
+            for (int bi = 0; bi < kSBlocks; ++bi)
+              aq[t][bi] = *reinterpret_cast<const uint4*>(asrc[bi] + kc + 16 * t);
+        };
+        auto compute = [&](const uint16_t* slot, const uint4 (&aq)[4][kSBlocks]) {
+          uint4 xo[4];  // the chunk's four x operands, read before the first MFMA
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            xo[t] = *reinterpret_cast<const uint4*>(&slot[orow * kSChunk + (((2 * t + (lane >> 5)) ^ (orow & 7)) << 3)]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint4 xv = make_uint4(xo[t].x & xmask, xo[t].y & xmask, xo[t].z & xmask, xo[t].w & xmask);
+#pragma unroll
+            for (int bi = 0; bi < kSBlocks; ++bi) {
+              const uint4 av = aq[t][bi];
+              acc[bi] = mfma32(make_uint4(av.x & amask[bi], av.y & amask[bi], av.z & amask[bi], av.w & amask[bi]), xv,
+                               acc[bi]);
             }
           }
+        };
+        issue(ring0, aq0, c0);
+        issue(ring1, aq1, c0 + 1);
+        for (int c = c0; c < c1; c += 2) {
+          MLORA_WAIT_VM(kSLoads);  // chunk c (x rows and A) has landed
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+          compute(ring0, aq0);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // its LDS reads are done before the slot is refilled
+          issue(ring0, aq0, c + 2);
+          if (c + 1 >= c1) break;
+          MLORA_WAIT_VM(kSLoads);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+          compute(ring1, aq1);
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          issue(ring1, aq1, c + 3);
         }
-        if (it + 1 < nk) stage(cur ^ 1);
-        if (it + 2 < nk) fetch((it + 2) * kSK);
-        __syncthreads();
+        MLORA_WAIT_VM(0);
       }
+      // the eight waves' sums in wave order, one 32-rank block at a time through LDS (the rings are free)
+      float* red = reinterpret_cast<float*>(s_ring0);  // [wave][register][lane]
 #pragma unroll
-      for (int m = 0; m < kMaxBlocks / 2; ++m) {
-        const int bi = half + 2 * m;
-        if (bi >= nbp) continue;
-        int j, kb;
-        rank_block(rk, L.n_mats, b0 + bi, j, kb);
-        const int n = kb * 32 + (lane & 31);
-        if (n >= rk[j]) continue;
-        uint16_t* out = mid + rank_offset(L, j) + n;
+      for (int bi = 0; bi < kSBlocks; ++bi) {
+        __syncthreads();  // every wave is done with the rings (and the previous block's sums)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int64_t p = p0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if (p >= sb && p < se) out[p * L.rank_cap] = f32_to_bf16(acc[m][i]);
+        for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc[bi][i];
+        __syncthreads();
+        if (b0 + bi < nblk) {
+          int j = 0, kb = 0;
+          rank_block(rk, L.n_mats, b0 + bi, j, kb);
+          for (int e = tid; e < 16 * kWave; e += kSWaves * kWave) {
+            const int i = e / kWave, ln = e % kWave;
+            float sum = red[i * kWave + ln];
+#pragma unroll
+            for (int w = 1; w < kSWaves; ++w) sum += red[(w * 16 + i) * kWave + ln];
+            const int n = kb * 32 + (i >> 2) * 8 + (ln >> 5) * 4 + (i & 3);
+            const int64_t p = p0 + (ln & 31);
+            if (n < rk[j] && p >= sb && p < se) mid[p * L.rank_cap + rank_offset(L, j) + n] = f32_to_bf16(sum);
+          }
         }
       }
     }
@@ -210,8 +246,9 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
                     uint16_t* mid, bool mfma, hipStream_t stream) {
   if (r.tokens == 0 || r.max_segs == 0) return MLORA_OK;
   if (mfma) {
-    const int64_t blocks = (r.tokens + kSM - 1) / kSM;
-    hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+    const int64_t blocks = (r.tokens + kSRows - 1) / kSRows;
+    hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks), dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k,
+                       mid);
   } else {
     int maxcap = 0;
     for (int j = 0; j < L.n_mats; ++j) maxcap = L.cap[j] > maxcap ? L.cap[j] : maxcap;
