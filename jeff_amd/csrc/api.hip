@@ -2,6 +2,7 @@
 // Every check runs on the host, before any launch; nothing here allocates, synchronises or reads device memory, so
 // the entry points can be recorded into a HIP graph.
 #include <climits>
+#include <mutex>
 
 #include "mlora_common.h"
 
@@ -109,6 +110,30 @@ size_t split_bytes(const mlora_int4_t* w, int64_t tokens) {
   return ((size_t)split_ranges(w, tokens) * (size_t)tokens * (size_t)w->columns * 4 + 255) & ~(size_t)255;
 }
 
+// A second stream and two events per device, made on the first split product: the split product's base launch runs
+// on it beside the first factor's launch (they only read x), and the epilogue launch waits for both. Default
+// priority; the fork and join are ordinary event waits, so a graph capture of the caller's stream records them.
+struct Aux {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool ok = false;
+};
+constexpr int kMaxDevices = 64;
+Aux g_aux[kMaxDevices];
+std::once_flag g_aux_once[kMaxDevices];
+
+const Aux* aux_stream() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_aux_once[dev], [dev] {
+    Aux& x = g_aux[dev];
+    x.ok = hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking) == hipSuccess &&
+           hipEventCreateWithFlags(&x.fork, hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x.join, hipEventDisableTiming) == hipSuccess;
+  });
+  return g_aux[dev].ok ? &g_aux[dev] : nullptr;
+}
+
 // The base product (and the LoRA second factor) once mid holds the first factors.
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
@@ -198,8 +223,24 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     return MLORA_EWORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* mid = static_cast<uint16_t*>(workspace);
-  if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, shrink_on_mfma(route, lora->pool_rows, flags), s)))
-    return rc;
+  const bool mfma_shrink = shrink_on_mfma(route, lora->pool_rows, flags);
+  if (base == Base::split) {
+    // split product: the base launch on the second stream beside the first factor's, then the epilogue
+    const Aux* aux = aux_stream();
+    if (aux == nullptr) return MLORA_ELAUNCH;
+    const int32_t ks = split_ranges(w, route->tokens);
+    float* part = static_cast<float*>(partials);
+    if (hipEventRecord(aux->fork, s) != hipSuccess || hipStreamWaitEvent(aux->stream, aux->fork, 0) != hipSuccess)
+      return MLORA_ELAUNCH;
+    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks,
+                             aux->stream)))
+      return rc;
+    if (hipEventRecord(aux->join, aux->stream) != hipSuccess) return MLORA_ELAUNCH;
+    if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
+    if (hipStreamWaitEvent(s, aux->join, 0) != hipSuccess) return MLORA_ELAUNCH;
+    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
+  }
+  if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
   return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, s);
 }
 
