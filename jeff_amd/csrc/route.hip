@@ -168,6 +168,114 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
   if (tid == 0) *r.status = status;
 }
 
+// Passes of at most 64 request rows: wave 0 routes them in registers (one request per lane, a bitonic sort of the
+// same keys by lane shuffles, prefix sums by shuffles), with one barrier before every wave writes the tokens. The
+// outputs are the block kernel's, bit for bit.
+constexpr int kSmallRequests = 64;
+
+__global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_t* __restrict__ adp,
+                                                                   const int32_t* __restrict__ cu, int32_t row_len,
+                                                                   mlora_route_t r, int32_t pool_rows) {
+  __shared__ int32_t s_start[kSmallRequests], s_len[kSmallRequests], s_ps[kSmallRequests];
+  __shared__ int32_t s_seg[kSmallRequests], s_q[kSmallRequests];
+  __shared__ int32_t s_ok;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = r.requests;
+  const int64_t T = r.tokens;
+  if (wave == 0) {
+    const bool live = lane < B;
+    int c0 = 0, c1 = 0;
+    bool bad = false;
+    if (cu != nullptr) {
+      if (live) {
+        c0 = cu[lane];
+        c1 = cu[lane + 1];
+        bad = c1 < c0;
+      }
+      if (lane == 0) bad = bad || cu[0] != 0 || (int64_t)cu[B] != T;
+    }
+    const bool seq_ok = __ballot(bad) == 0;
+    int a = live ? adp[lane] : 0;
+    const bool bad_a = live && (a < 0 || a >= pool_rows);
+    if (bad_a) a = 0;
+    const int len = cu != nullptr ? c1 - c0 : row_len;
+    const int start = cu != nullptr ? c0 : lane * row_len;
+    uint32_t key = live ? (((uint32_t)a << kIndexBits) | (uint32_t)lane) : 0xFFFFFFFFu;  // padding sorts last
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t other = __shfl_xor(key, j);
+        const bool up = (lane & k) == 0, lower = (lane & j) == 0;
+        key = (lower == up) ? min(key, other) : max(key, other);
+      }
+    const int q = (int)(key & ((1u << kIndexBits) - 1));  // the request at sorted position `lane`
+    const int ada = (int)(key >> kIndexBits);
+    const int qlen_any = __shfl(len, q & 63);  // every lane takes part in the shuffle
+    const int qlen = live ? qlen_any : 0;
+    const int qstart = __shfl(start, q & 63);
+    const int prev = __shfl_up(ada, 1);
+    const bool first = live && (lane == 0 || prev != ada);
+    int lsum = qlen, fsum = first ? 1 : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int yl = __shfl_up(lsum, o), yf = __shfl_up(fsum, o);
+      if (lane >= o) {
+        lsum += yl;
+        fsum += yf;
+      }
+    }
+    const int pstart = lsum - qlen, seg = fsum - 1;
+    const int nseg = __shfl(fsum, 63), total = __shfl(lsum, 63);
+    const bool any_bad_adapter = __ballot(bad_a) != 0;  // every lane takes part in the vote
+    if (seq_ok) {
+      if (live) {
+        r.req_order[lane] = q;
+        if (first) {
+          r.seg_adapter[seg] = ada;
+          r.seg_start[seg] = pstart;
+        }
+        s_start[lane] = qstart;
+        s_len[lane] = qlen;
+        s_ps[lane] = pstart;
+        s_seg[lane] = seg;
+        s_q[lane] = q;
+      }
+      if (lane == 0) {
+        *r.num_segs = nseg;
+        r.seg_start[nseg] = total;
+        *r.status = any_bad_adapter ? MLORA_ROUTE_BAD_ADAPTER : 0;
+      }
+    }
+    if (lane == 0) s_ok = seq_ok ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_ok) {  // unusable offsets: identity routing through row 0 (no LoRA), flagged
+    for (int64_t p = tid; p < T; p += kRouteThreads) {
+      r.tok_perm[p] = (int32_t)p;
+      r.last_of[p] = -1;
+      r.seg_of[p] = 0;
+    }
+    for (int i = tid; i < B; i += kRouteThreads) r.req_order[i] = i;
+    if (tid == 0) {
+      *r.num_segs = 1;
+      r.seg_start[0] = 0;
+      r.seg_start[1] = (int32_t)T;
+      r.seg_adapter[0] = 0;
+      *r.status = MLORA_ROUTE_BAD_SEQLENS;
+    }
+    return;
+  }
+  for (int i = wave; i < B; i += kRouteThreads / 64) {  // one request per wave, its tokens across the lanes
+    const int start = s_start[i], l = s_len[i], ps = s_ps[i], sg = s_seg[i], q = s_q[i];
+    for (int t = lane; t < l; t += 64) {
+      r.tok_perm[ps + t] = start + t;
+      r.last_of[ps + t] = t == l - 1 ? q : -1;
+      r.seg_of[ps + t] = sg;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void dequant_kernel(mlora_int4_t w, uint16_t* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int words_per_col = w.k / 8;
@@ -184,7 +292,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(mlora_int4_t w, uint16_t* 
 
 int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const mlora_route_t& r, int32_t pool_rows,
                  hipStream_t stream) {
-  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
+  if (r.requests <= kSmallRequests)
+    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
+  else
+    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }
 

@@ -60,8 +60,8 @@ def assert_route_equal(ws: Workspace, tokens: int, want: dict, requests: int) ->
     assert int(ws.status.item()) == want["status"]
 
 
-@pytest.mark.parametrize("case", ["uniform-32", "decode-256", "one-row", "ragged-64", "zipf-512", "empty-rows",
-                                  "all-base", "single-adapter", "out-of-range", "max-requests"])
+@pytest.mark.parametrize("case", ["uniform-32", "decode-256", "one-row", "ragged-64", "ragged-65", "zipf-512",
+                                  "empty-rows", "all-base", "single-adapter", "out-of-range", "max-requests"])
 def test_route_is_bit_exact(case: str) -> None:
     rng = np.random.default_rng(hash(case) % 2**32)
     cu = None
@@ -73,9 +73,10 @@ def test_route_is_bit_exact(case: str) -> None:
         adp = rng.integers(1, 65, 256)
     elif case == "one-row":
         adp, row_len = np.array([3]), 16
-    elif case == "ragged-64":
-        adp = rng.integers(1, 17, 64)
-        cu = np.concatenate([[0], np.cumsum(rng.integers(16, 257, 64))])
+    elif case in ("ragged-64", "ragged-65"):  # the one-wave and the block routing kernels
+        n = int(case[-2:])
+        adp = rng.integers(1, 17, n)
+        cu = np.concatenate([[0], np.cumsum(rng.integers(16, 257, n))])
     elif case == "zipf-512":
         p = np.arange(1, 129) ** -1.1
         adp = rng.choice(128, 512, p=p / p.sum()) + 1
