@@ -93,7 +93,7 @@ __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int
 }
 
 constexpr int kSRows = 32;    // sorted rows per workgroup
-constexpr int kSWaves = 8;    // waves per workgroup, each a contiguous share of the inputs
+constexpr int kSWaves = 4;    // waves per workgroup, each a contiguous share of the inputs (two workgroups per CU)
 constexpr int kSBlocks = 2;   // 32-rank blocks per pass
 constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
 constexpr int kSLoads = 4 + 4 * kSBlocks;  // memory instructions per chunk and lane: x rows to LDS, then A
@@ -106,11 +106,11 @@ __shared__ __attribute__((aligned(16))) uint16_t s_ring1[kSWaves * kSRows * kSCh
 
 #define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
 
-// Long segments (prefill): one workgroup per 32 sorted rows; its 8 waves split the input dimension into chunks of
+// Long segments (prefill): one workgroup per 32 sorted rows; its 4 waves split the input dimension into chunks of
 // 64. A wave streams its chunks of the 32 x rows (gathered through the sorted order) into its own LDS ring with
 // buffer loads that cover whole 128-byte rows, one chunk ahead, and loads the matching A operands into registers
 // one chunk ahead; one 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's
-// accumulators hold four consecutive ranks of one token. The eight partial sums are added in wave order in LDS
+// accumulators hold four consecutive ranks of one token. The four partial sums are added in wave order in LDS
 // and rounded once. Rows outside the segment read zero x operands.
 __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
                                                                   const uint16_t* __restrict__ x, int64_t x_stride,
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
         }
         MLORA_WAIT_VM(0);
       }
-      // the eight waves' sums in wave order, one 32-rank block at a time through LDS (the rings are free)
+      // the waves' sums in wave order, one 32-rank block at a time through LDS (the rings are free)
       float* red = reinterpret_cast<float*>(s_ring0);  // [wave][register][lane]
 #pragma unroll
       for (int bi = 0; bi < kSBlocks; ++bi) {
