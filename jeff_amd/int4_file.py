@@ -1,0 +1,197 @@
+"""INT4 checkpoint ingestion: an INT4 base's `int4.safetensors` read into the kernel layout.
+
+Restates the reference's strict reader (engine/int4.py:280-325, `_check_matrix` and `read_int4_file`) and its writer
+of the same file (engine/int4.py:398-464, the int4.safetensors part):
+- per matrix `<name>.qweight` uint8 (out, in/2): two integers per byte, low nibble first, each stored as q + 8
+  (the reference's format "int4-g64": q in [-8, 7], no zero point);
+- `<name>.scales` bfloat16 (out, in/G), finite and positive;
+- the file must be the one its record names (sha256) and hold exactly those tensors, nothing else.
+
+Extension for the asymmetric configurations (absent from the reference's format): an optional `<name>.zeros` uint8
+(out, in/G) of zero points in [0, 15] (the stored byte then holds the code c itself, weight bf16((c - z) s)), and
+groups of G = 64 or 128 inputs, G read from the scales' shape. A file without zeros and with G = 64 is exactly the
+reference's. Reading never executes anything from the file (safetensors)."""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import tempfile
+from collections.abc import Mapping, Sequence
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+from safetensors.torch import load_file, save_file
+
+from jeff_amd.int4 import GROUPS, Int4Error, KernelInt4, dequantize, pack_kernel, pack_kernel_asym, unpack_int4
+
+INT4_FILE = "int4.safetensors"  # engine/int4.py:45
+
+
+@dataclass(frozen=True)
+class StoredInt4:
+    """One matrix as stored: qweight uint8 (out, in/2), scales bf16 (out, in/G), zeros uint8 (out, in/G) or None."""
+    qweight: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor | None = None
+
+    @property
+    def group(self) -> int:
+        return 2 * self.qweight.shape[1] // self.scales.shape[1]
+
+
+def file_sha256(path: Path) -> str:
+    """engine/int4.py:71-73: the sha256 of a file, 64 lower-case hex digits."""
+    digest = hashlib.sha256()
+    with Path(path).open("rb") as stream:
+        for block in iter(lambda: stream.read(1 << 24), b""):
+            digest.update(block)
+    return digest.hexdigest()
+
+
+def check_matrix(name: str, shape: tuple[int, int], m: StoredInt4) -> None:
+    """engine/int4.py:280-295 (plus the zero-point extension): Int4Error naming what is wrong with one stored matrix
+    of `shape` (out, in)."""
+    out, inputs = shape
+    if m.qweight.dtype != torch.uint8:
+        raise Int4Error(f"{INT4_FILE}: {name}.qweight is {m.qweight.dtype}; it must be uint8, two 4-bit integers per "
+                        "byte stored as q + 8 (so every integer is in [-8, 7]): integers stored any other way can be "
+                        "out of range")
+    if tuple(m.qweight.shape) != (out, inputs // 2):
+        raise Int4Error(f"{INT4_FILE}: {name}.qweight has shape {tuple(m.qweight.shape)}; the {out} x {inputs} matrix "
+                        f"needs ({out}, {inputs // 2})")
+    if m.scales.dtype != torch.bfloat16:
+        raise Int4Error(f"{INT4_FILE}: {name}.scales is {m.scales.dtype}; it must be bfloat16")
+    groups = [g for g in GROUPS if inputs % g == 0 and tuple(m.scales.shape) == (out, inputs // g)]
+    if not groups:
+        raise Int4Error(f"{INT4_FILE}: {name}.scales has shape {tuple(m.scales.shape)}; the {out} x {inputs} matrix "
+                        f"needs ({out}, {inputs} / G), one scale per G inputs, G in {GROUPS}")
+    if not bool(torch.isfinite(m.scales).all()) or not bool((m.scales > 0).all()):
+        raise Int4Error(f"{INT4_FILE}: {name}.scales holds a scale that is not finite and positive")
+    if m.zeros is not None:
+        if m.zeros.dtype != torch.uint8 or tuple(m.zeros.shape) != tuple(m.scales.shape):
+            raise Int4Error(f"{INT4_FILE}: {name}.zeros must be uint8 of the scales' shape {tuple(m.scales.shape)}; "
+                            f"got {m.zeros.dtype} {tuple(m.zeros.shape)}")
+        if bool((m.zeros > 15).any()):
+            raise Int4Error(f"{INT4_FILE}: {name}.zeros holds a zero point above 15")
+
+
+def read_int4_file(path: Path, int4_sha256: str | None, matrices: Mapping[str, tuple[int, int]]
+                   ) -> dict[str, StoredInt4]:
+    """engine/int4.py:298-325: {matrix name: StoredInt4} from `path`, every tensor checked. The file must have the
+    sha256 the record names (`int4_sha256`; None skips the check, for files this build wrote itself) and hold exactly
+    the qweight and scales (and, for the asymmetric extension, zeros) of each of `matrices` (name -> (out, in))."""
+    path = Path(path)
+    if not path.is_file():
+        raise Int4Error(f"{path} does not exist: an INT4 base keeps its matrices in {INT4_FILE}")
+    if int4_sha256 is not None:
+        digest = file_sha256(path)
+        if digest != int4_sha256:
+            raise Int4Error(f"{path} has sha256 {digest}, but the record names {int4_sha256}: the file is not the one "
+                            "this INT4 base was made with")
+    packed = load_file(str(path))
+    wanted = {f"{name}.{part}" for name in matrices for part in ("qweight", "scales")}
+    absent = sorted(wanted - set(packed))
+    if absent:
+        raise Int4Error(f"{path} lacks {len(absent)} tensors ({', '.join(absent[:3])}"
+                        f"{', ...' if len(absent) > 3 else ''}): each INT4 matrix needs its qweight and scales")
+    zeros = {f"{name}.zeros" for name in matrices} & set(packed)
+    surplus = sorted(set(packed) - wanted - zeros)
+    if surplus:
+        raise Int4Error(f"{path} holds {len(surplus)} tensors that are not an INT4 matrix's qweight, scales or zeros "
+                        f"({', '.join(surplus[:3])}{', ...' if len(surplus) > 3 else ''})")
+    found = {}
+    for name, shape in matrices.items():
+        m = StoredInt4(packed[f"{name}.qweight"], packed[f"{name}.scales"], packed.get(f"{name}.zeros"))
+        check_matrix(name, shape, m)
+        found[name] = m
+    return found
+
+
+def write_int4_file(path: Path, matrices: Mapping[str, StoredInt4]) -> str:
+    """Write `matrices` as an int4.safetensors at `path` (to a temporary file beside it, then renamed, as the
+    reference writes its folders: engine/int4.py:449-464) and return the file's sha256 for the record."""
+    path = Path(path)
+    tensors: dict[str, torch.Tensor] = {}
+    for name, m in matrices.items():
+        inputs = 2 * m.qweight.shape[1]
+        check_matrix(name, (m.qweight.shape[0], inputs), m)
+        tensors[f"{name}.qweight"] = m.qweight.contiguous().cpu()
+        tensors[f"{name}.scales"] = m.scales.contiguous().cpu()
+        if m.zeros is not None:
+            tensors[f"{name}.zeros"] = m.zeros.contiguous().cpu()
+    path.parent.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix=".int4-", suffix=".partial", dir=path.parent)
+    os.close(fd)
+    try:
+        save_file(tensors, tmp)
+        os.replace(tmp, path)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return file_sha256(path)
+
+
+def stored_from_codes(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor | None = None) -> StoredInt4:
+    """A matrix's stored form from its codes c in [0, 15] (out, in), bf16 scales and optional uint8 zero points:
+    the bytes hold codes low nibble first (without zeros the codes are q + 8, the reference's storage)."""
+    if codes.dtype != torch.uint8 or codes.dim() != 2 or codes.shape[1] % 2 or bool((codes > 15).any()):
+        raise Int4Error("codes must be a uint8 (out, in) tensor of values in [0, 15] with an even number of inputs")
+    qweight = (codes[:, 0::2] | (codes[:, 1::2] << 4)).contiguous()
+    return StoredInt4(qweight, scales, zeros)
+
+
+def _codes(m: StoredInt4) -> torch.Tensor:
+    """The codes c in [0, 15] of a stored matrix (out, in)."""
+    low, high = m.qweight & 0xF, m.qweight >> 4
+    return torch.stack([low, high], dim=2).reshape(m.qweight.shape[0], -1)
+
+
+def dequantize_stored(m: StoredInt4) -> torch.Tensor:
+    """bf16((c - z) s) of a stored matrix (z = 8 without zeros: the reference's bf16(q * s)), on its device."""
+    if m.zeros is None:
+        return dequantize(unpack_int4(m.qweight), m.scales, m.group)
+    return dequantize(_codes(m), m.scales, m.group, m.zeros)
+
+
+def pack_stored_group(stored: Mapping[str, StoredInt4], names: Sequence[str], device: torch.device | str,
+                      dequantised: torch.Tensor | None = None) -> KernelInt4:
+    """engine/int4.py:265-277: the kernel layout of a fused group, the matrices `names` stacked along the output in
+    that order, packed on `device`. When the group's bfloat16 weights are given (the standard path's copy), they must
+    be bf16((c - z) s) of the same integers, zero points and scales bit for bit; Int4Error naming the group
+    otherwise. Every matrix of a group must share its group size and either all or none carry zero points."""
+    ms = [stored[name] for name in names]
+    groups = {m.group for m in ms}
+    if len(groups) != 1:
+        raise Int4Error(f"{', '.join(names)}: the matrices of a fused group must share one group size; got "
+                        f"{sorted(groups)}")
+    group = groups.pop()
+    asym = {m.zeros is not None for m in ms}
+    if len(asym) != 1:
+        raise Int4Error(f"{', '.join(names)}: either every matrix of a fused group has zero points or none has")
+    ms = [StoredInt4(m.qweight.to(device), m.scales.to(device), None if m.zeros is None else m.zeros.to(device))
+          for m in ms]
+    if dequantised is not None:
+        want = torch.cat([dequantize_stored(m) for m in ms])
+        if dequantised.dtype != torch.bfloat16 or not torch.equal(want, dequantised.to(device)):
+            raise Int4Error(f"The bfloat16 weights of {', '.join(names)} are not bf16((c - z) s) of their integers and "
+                            f"scales in {INT4_FILE}")
+    scales = torch.cat([m.scales for m in ms])
+    if ms[0].zeros is None:
+        return pack_kernel(torch.cat([unpack_int4(m.qweight) for m in ms]), scales, group)
+    return pack_kernel_asym(torch.cat([_codes(m) for m in ms]), scales, torch.cat([m.zeros for m in ms]), group)
+
+
+def attach_int4_file(lins: Sequence, path: Path, int4_sha256: str | None, device: torch.device | str = "cuda",
+                     check_weights: bool = True) -> None:
+    """fast_path.py:352-363 from a file: give every fused group (Lin) its kernel layout read from `path`, checked
+    against the group's bfloat16 weights (lin.W) when it has them and `check_weights` is set."""
+    matrices = {}
+    for lin in lins:
+        for name, n in zip(lin.names, lin.sizes):
+            matrices[name] = (n, lin.k)
+    stored = read_int4_file(path, int4_sha256, matrices)
+    for lin in lins:
+        w = lin.W if (check_weights and getattr(lin, "W", None) is not None) else None
+        lin.int4 = pack_stored_group(stored, lin.names, device, w)
