@@ -18,6 +18,8 @@
  *   mlora_dequant      dequantize / bf16(q * s) of the kernel layout       int4.py:203-208,258-262
  *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
  *   mlora_int4_partials_bytes  Workspace.P sizing (split partial products)  int4_kernels.py:150-166
+ *   mlora_readout_logits  readout_logits (per-adapter readout)          batched_kernels.py:492-504,522-536
+ *   mlora_option_softmax  option_softmax (mask, temperature, softmax)     batched_kernels.py:507-519,539-553
  */
 #ifndef JEFF_MLORA_H
 #define JEFF_MLORA_H
@@ -33,6 +35,8 @@ extern "C" {
 #define MLORA_MAX_MATS 8            /* matrices per fused group (the reference's largest has 4) */
 #define MLORA_MAX_REQUESTS 8192     /* request rows per routed pass */
 #define MLORA_MAX_POOL_ROWS 262144  /* adapter pool rows (row 0 = the base, no update) */
+#define MLORA_READOUT_MAX_DIM 2048  /* hidden size of the decision head's readout */
+#define MLORA_READOUT_MAX_OPTIONS 256  /* answer options per readout */
 
 enum {
   MLORA_OK = 0,
@@ -149,6 +153,20 @@ int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, cons
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,
                    int32_t k, uint16_t* y, int64_t y_stride, int32_t n_out, void* workspace, size_t workspace_bytes,
                    int32_t flags, void* stream);
+
+/* The decision head's logits (the reference's readout_logits): for each of `rows` request rows, logits (rows,
+ * options) float32 = bf16(sum_d readout_pool[adapters[b]][o][d] * hidden[b][d]) summed in float32. hidden bf16 (rows,
+ * dim) rows hidden_stride apart; readout_pool bf16 (pool_rows, options, dim), adapters pool_stride elements apart;
+ * adapters int32 (rows), an index outside [0, pool_rows) reads row 0. dim a multiple of 8, at most
+ * MLORA_READOUT_MAX_DIM; options at most MLORA_READOUT_MAX_OPTIONS. */
+int mlora_readout_logits(const uint16_t* hidden, int64_t hidden_stride, int32_t dim, const uint16_t* readout_pool,
+                         int64_t pool_stride, int32_t options, int32_t pool_rows, const int32_t* adapters,
+                         int32_t rows, float* logits, void* stream);
+
+/* The decision head's probabilities (the reference's option_softmax): probs (rows, options) float32 = softmax over o
+ * of (o < counts[b] ? logits[b][o] : -1e9) / temp_pool[adapters[b]]; temp_pool float32 (pool_rows). */
+int mlora_option_softmax(const float* logits, int32_t options, const int32_t* adapters, const int32_t* counts,
+                         const float* temp_pool, int32_t pool_rows, int32_t rows, float* probs, void* stream);
 
 #ifdef __cplusplus
 }

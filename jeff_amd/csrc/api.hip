@@ -281,5 +281,29 @@ int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const u
   return launch_base(nullptr, *lora, *route, x, x_stride, y, y_stride, nullptr, n_out, mid, gemv, s);
 }
 
+int mlora_readout_logits(const uint16_t* hidden, int64_t hidden_stride, int32_t dim, const uint16_t* readout_pool,
+                         int64_t pool_stride, int32_t options, int32_t pool_rows, const int32_t* adapters,
+                         int32_t rows, float* logits, void* stream) {
+  if (rows < 0 || dim <= 0 || options <= 0 || pool_rows < 1) return MLORA_EINVAL;
+  if (dim % 8 || dim > MLORA_READOUT_MAX_DIM || options > MLORA_READOUT_MAX_OPTIONS) return MLORA_EUNSUPPORTED;
+  if (rows == 0) return MLORA_OK;
+  if (hidden == nullptr || readout_pool == nullptr || adapters == nullptr || logits == nullptr) return MLORA_EINVAL;
+  if (hidden_stride < dim || pool_stride < (int64_t)options * dim) return MLORA_EINVAL;
+  if (!aligned16(hidden) || !aligned16(readout_pool) || hidden_stride % 8 || pool_stride % 8) return MLORA_EALIGN;
+  return launch_readout_logits(hidden, hidden_stride, dim, readout_pool, pool_stride, options, pool_rows, adapters,
+                               rows, logits, static_cast<hipStream_t>(stream));
+}
+
+int mlora_option_softmax(const float* logits, int32_t options, const int32_t* adapters, const int32_t* counts,
+                         const float* temp_pool, int32_t pool_rows, int32_t rows, float* probs, void* stream) {
+  if (rows < 0 || options <= 0 || pool_rows < 1) return MLORA_EINVAL;
+  if (options > MLORA_READOUT_MAX_OPTIONS) return MLORA_EUNSUPPORTED;
+  if (rows == 0) return MLORA_OK;
+  if (logits == nullptr || adapters == nullptr || counts == nullptr || temp_pool == nullptr || probs == nullptr)
+    return MLORA_EINVAL;
+  return launch_option_softmax(logits, options, adapters, counts, temp_pool, pool_rows, rows, probs,
+                               static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
 #pragma GCC visibility pop

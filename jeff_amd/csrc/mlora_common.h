@@ -123,6 +123,12 @@ __device__ __forceinline__ int matrix_of(const mlora_lora_t& L, int c) {
 
 }  // namespace mlora
 
+// The decision head: option logits per row from its adapter's readout; the masked, tempered softmax.
+int launch_readout_logits(const uint16_t* hidden, int64_t hidden_stride, int32_t dim, const uint16_t* pool,
+                          int64_t pool_stride, int32_t options, int32_t pool_rows, const int32_t* adapters,
+                          int32_t rows, float* logits, hipStream_t stream);
+int launch_option_softmax(const float* logits, int32_t options, const int32_t* adapters, const int32_t* counts,
+                          const float* temp_pool, int32_t pool_rows, int32_t rows, float* probs, hipStream_t stream);
 // The split product's second launch stages its rows' first factors in LDS: at most this stacked rank.
 #define MLORA_SPLIT_MAX_RANK 512
 

@@ -11,6 +11,8 @@ Modules (each function cites the reference file:line it restates; paths are rela
              `bf16((c - z) * s)` (`engine/int4.py:203-208`, `engine/int4_kernels.py:57-59`), g64 or g128, zeros.
 - `routing`: adapter id per request row -> stable segment sort (replaces `adp[t // row_len]`,
              `engine/fast_path.py:167,189`).
+- `readout`: the decision head, per-adapter readout logits rounded to bfloat16 and the masked, tempered softmax
+             (`engine/batched_kernels.py:492-559`).
 - `layer`:   the reference's torch layer `LoraLinear.forward` applied per adapter segment (`engine/lora.py:204-220`)
              in "model" and "float32" precision; the float64 exact result and the forward error bounds of
              `tests/test_int4_kernels_cuda.py:108-168`.
@@ -25,4 +27,8 @@ How each function is pinned (checked by `tests/test_oracle_*.py` against golden 
 - routing: invariants (bijection, stable order, one adapter per segment, coverage) and equality with
   `adp[t // row_len]` on uniform rows, brute force on tiny inputs.
 - layer: the float64 exact result against an independent per-element sum; the bound model is the reference's own.
+- readout: logits against a per-element sum in exact rationals on small inputs (and so the rounding through float32
+  to bfloat16 on every value), planted mistakes (another adapter's readout, a transposed readout); the softmax against
+  closed forms (one option kept gives 1, equal logits give 1/count, a temperature t equals logits divided by t at
+  temperature 1), torch's float32 softmax, and the reference's mask value -1e9.
 """
