@@ -3,7 +3,8 @@
 of its dominant kernel, with the CPU restatement of the reference's torch layer timed beside it.
 
 A step is one pass over one batch: route the request rows by adapter, then every fused group of every layer
-(int4_product: LoRA first factor, then the INT4 base product with the second factor fused). The step is recorded once
+(int4_product: LoRA first factor, then the INT4 base product with the second factor fused) and, where the workload
+gathers each request's last-token output (prefill-skewed-28l), the decision head on it. The step is recorded once
 as a HIP graph and replayed. Inputs (weights, adapter pool, activations) are resident in HBM before timing.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
@@ -86,6 +87,7 @@ def main() -> int:
     from jeff_amd.fast_path import DT, Workspace
     from jeff_amd.int4_kernels import base_expand, int4_product, shrink
     from jeff_amd.int4_tiles import int4_tiles
+    from jeff_amd.readout import readout_rows
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -112,6 +114,9 @@ def main() -> int:
                 x = xs[(li if per_layer_acts else 0, label)]
                 gather = last if (last is not None and li == len(w.layers) - 1 and label == "down") else None
                 keep.append(int4_product(lin, x, ws, w.adp, last_out=gather))
+        if w.readout is not None:  # the decision head on each request's last-token output
+            keep.append(readout_rows(last, w.readout["readout_pool"], w.readout["temp_pool"], w.adp,
+                                     w.readout["counts"]))
         if len(keep) > 8:
             del keep[:-8]
 
@@ -195,12 +200,38 @@ def main() -> int:
                  "hbm_frac": step_bytes / (ms_per_step / 1e3) / PEAK_HBM,
                  "flops": step_flops, "bytes": step_bytes}
 
+    head = None
+    if w.readout is not None:  # the decision head alone: its two launches, timed as the dominant kernel is
+        r = w.readout
+        hreps = 50
+        hgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(hgraph):
+            for _ in range(hreps):
+                readout_rows(last, r["readout_pool"], r["temp_pool"], w.adp, r["counts"])
+        hgraph.replay()
+        torch.cuda.synchronize()
+        head_ms = []
+        for _ in range(3):
+            e0.record(stream)
+            hgraph.replay()
+            e1.record(stream)
+            e1.synchronize()
+            head_ms.append(e0.elapsed_time(e1) / hreps)
+        hms = statistics.median(head_ms)
+        hbytes = workloads.readout_bytes(w)
+        head = {"kernels": "readout_logits_kernel + option_softmax_kernel", "ms": hms, "bytes": hbytes,
+                "hbm_frac": hbytes / (hms / 1e3) / PEAK_HBM, "rows": w.requests,
+                "options": int(r["readout_pool"].shape[1]), "dim": int(r["readout_pool"].shape[2])}
+        del hgraph
+
     cpu = None if args.no_cpu else cpu_baseline(w, xs, per_layer_acts, args.cpu_seconds)
     del graph, kgraph
     config = {"workload": args.workload, "tokens": w.tokens, "requests": w.requests, "layers": len(w.layers),
               "groups": {k: [v.k, v.out] for k, v in w.layers[0].items()},
               "adapters": len(w.adapter_ranks), "ranks": sorted(set(w.adapter_ranks.values())),
               "group_size": 128, "zero_points": True, "step_roofline": step_roof}
+    if head is not None:
+        config["decision_head"] = head
     print(json.dumps({"metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                       "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
                       "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded; random INT4 weights and "

@@ -6,7 +6,9 @@ A workload is a set of fused groups (Lin) with INT4 weights and an adapter pool,
 - "decode-28l": 28 layers x {qkv 2048->4096, o 2048->2048, gate_up 2048->12288, down 6144->2048}, 256 one-token
   rows, 64 adapters with ranks 8/16/32/64 (16 each), adapter per row uniform;
 - "prefill-skewed-28l": the same layers, 512 requests with lengths LogNormal(ln 200, 1) clipped to [16, 2048],
-  128 adapters of rank 32 chosen with Zipf(1.1) popularity, each request's last-token output gathered;
+  128 adapters of rank 32 chosen with Zipf(1.1) popularity, each request's last-token output gathered for the
+  decision head (a readout of 255 options x 2048 per adapter row, bf16 0.05 N(0, 1); temperatures U(0.5, 2); option
+  counts uniform in [1, 255]);
 - "decode-pool-28l": the same layers, 4096 one-token rows, 1024 adapters of rank 64 all resident, uniform ids.
 Weights: codes uniform in [0, 15], zero points uniform in [0, 15], bf16 scales U(0.005, 0.02), 128 inputs per
 group. LoRA: A ~ N(0, (1/32)^2), B ~ N(0, 0.02^2), scale alpha/r = 2 folded into B. x ~ N(0, 1) bf16."""
@@ -30,6 +32,7 @@ GROUPS_28L = {  # label: (matrix names, outputs, inputs)
     "down": (["mlp.down_proj"], [HIDDEN], INTER),
 }
 SIGMA_A, SIGMA_B, LORA_SCALE = 1.0 / 32, 0.02, 2.0
+READOUT_OPTIONS = 255  # the decision head's options (engine/batched_kernels.py READOUT_ROWS)
 
 
 @dataclass
@@ -44,6 +47,7 @@ class Workload:
     lengths: np.ndarray
     adapter_ranks: dict[int, int]         # pool row -> rank of every adapted matrix
     gather_last: bool = False
+    readout: dict | None = None           # decision head: readout_pool, temp_pool, counts (gather_last workloads)
     notes: dict = field(default_factory=dict)
 
 
@@ -132,11 +136,18 @@ def make(name: str, device: str = "cuda", seed: int = 0, n_layers: int | None = 
         raise ValueError(f"unknown workload {name!r}")
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     ragged = not bool((lengths == 1).all())
+    readout = None
+    if gather:
+        dim, rows = layers[-1]["down"].out, pool.lora_pool.shape[0]
+        readout = {"readout_pool": (0.05 * torch.randn(rows, READOUT_OPTIONS, dim, generator=gen, device=device)).to(DT),
+                   "temp_pool": 0.5 + 1.5 * torch.rand(rows, generator=gen, device=device),
+                   "counts": torch.tensor(rng.integers(1, READOUT_OPTIONS + 1, len(lengths)).astype(np.int32),
+                                          device=device)}
     return Workload(name=name, layers=layers, pool=pool,
                     adp=torch.tensor(ids.astype(np.int32), device=device),
                     cu_seqlens=torch.tensor(cu, device=device) if ragged else None,
                     tokens=int(cu[-1]), requests=len(lengths), lengths=lengths, adapter_ranks=ranks,
-                    gather_last=gather)
+                    gather_last=gather, readout=readout)
 
 
 def inputs(w: Workload, label: str, gen: torch.Generator | None = None) -> torch.Tensor:
@@ -178,4 +189,15 @@ def hbm_bytes(w: Workload) -> float:
                 total += sum(2.0 * min(r, c) * (lin.k + n) for n, c in zip(lin.sizes, lin.caps) if c)
     if w.gather_last:
         total += 2.0 * w.requests * w.layers[-1]["down"].out
+    if w.readout is not None:
+        total += readout_bytes(w)
     return total
+
+
+def readout_bytes(w: Workload) -> float:
+    """Algorithmic HBM bytes of the decision head: the readout of every adapter row present once, each request's
+    hidden row in, its logits out and back in (float32) and its probabilities out (float32)."""
+    pool = w.readout["readout_pool"]
+    present = len({int(a) for a in w.adp.cpu().tolist()})
+    options, dim = pool.shape[1], pool.shape[2]
+    return 2.0 * present * options * dim + w.requests * (2.0 * dim + 3 * 4.0 * options)
