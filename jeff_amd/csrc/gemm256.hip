@@ -11,8 +11,9 @@
 //    consecutive inputs of one column that a 32x32x16 operand lane holds), one step ahead, with the raw scale and
 //    zero point of its columns, and dequantises them to bf16((c - z) s) in registers, the next 16 inputs' words
 //    interleaved with the current MFMAs. The two waves sharing a column range both dequantise it.
-// With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: an LDS-only barrier after an
-// explicit wait for the x rows of the next step (a __syncthreads() would also wait for the rows two steps ahead).
+// With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: a bare barrier after an
+// explicit wait for the x rows of the next step (a __syncthreads(), or any release fence, would also wait for the
+// rows two steps ahead).
 // LDS rows are 128 bytes (64 bf16) with their eight 16-byte chunks XOR-swizzled by (row & 7): the 16-byte operand
 // reads of 8 consecutive rows hit 8 distinct chunk positions, i.e. all banks once. The ring buffers are distinct LDS
 // arrays chosen at compile time (the loop is unrolled by six). Tiles are ordered so that the column tiles of one
@@ -54,6 +55,17 @@ __device__ __forceinline__ void lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Step barrier of the main loop, where LDS is written only by the x loads and only read by the waves. The wave's
+// own x loads of the next step have landed (MLORA_WAIT_VM before this); its LDS reads are drained inside the asm
+// statement, so none can be scheduled between the drain and the barrier; then the barrier. There is no release fence:
+// a fence would also wait for the x loads in flight for two steps ahead. The memory clobbers keep the compiler from
+// moving LDS reads or loads across the barrier.
+__device__ __forceinline__ void step_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // blockIdx -> tile index such that consecutive tiles share an XCD (blocks are dealt to the 8 XCDs round-robin)
@@ -159,11 +171,13 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x16_t{};
 
+  // (indexed as 16-byte elements of the buffer: each read's address is then one index into the LDS array, which
+  // keeps the compiler's knowledge of which array it reads, so it does not wait for x loads into the other buffers)
   auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[4]) {
     const int c = 2 * k16 + (lane >> 5);
+    const uint4* xv = reinterpret_cast<const uint4*>(xs);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-      a[mb] = *reinterpret_cast<const uint4*>(&xs[swz(wm * 128 + mb * 32 + (lane & 31), c)]);
+    for (int mb = 0; mb < 4; ++mb) a[mb] = xv[swz(wm * 128 + mb * 32 + (lane & 31), c) >> 3];
   };
   // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. The A
   // reads and the dequantisation of the next 16 inputs are interleaved with the current 16 inputs' MFMAs (one MFMA,
@@ -209,27 +223,29 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
   // Step i reads x buffer i % 3 (its rows loaded at the start of step i - 2) and weight set i % 2 (loaded at the
   // start of step i - 1). Every load is unconditional (past the last step it re-reads the last one into a buffer or
-  // set that is never used), so the number of loads in flight at each wait is the same on every path:
-  // after x(i + 1) come w(i), x(i + 2) and w(i + 1).
+  // set that is never used), so the number of loads in flight at each wait is the same on every path. Each step
+  // issues its weights before its x rows: loads complete in order, so waiting for the weights of step i + 1 does not
+  // wait for the x rows of step i + 2. After x(i + 1) come w(i + 1) and x(i + 2).
   const int nk = w.k / kTK / ksplit;  // this block's K steps, from step ks * nk
   const int kbase = ks * nk * kTK;
   WStage s0, s1;
-  dma_x(g_x0, kbase);
   fetch_w(s0, kbase);
+  dma_x(g_x0, kbase);
   dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
-  MLORA_WAIT_VM(kWLoads + kXLoads);  // x(0) has landed
-  lds_sync();
+  MLORA_WAIT_VM(kXLoads);  // x(0) has landed
+  step_sync();
   auto run = [&](auto xb, auto wb, int i) {
     constexpr int XB = decltype(xb)::value, WB = decltype(wb)::value;
     const uint16_t* xs = XB == 0 ? g_x0 : XB == 1 ? g_x1 : g_x2;
     uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;  // buffer (i + 2) % 3
     WStage& cur = WB == 0 ? s0 : s1;
     WStage& nxt = WB == 0 ? s1 : s0;
-    dma_x(xf, kbase + min(i + 2, nk - 1) * kTK);
     fetch_w(nxt, kbase + min(i + 1, nk - 1) * kTK);
+    __builtin_amdgcn_sched_barrier(0);  // keep every weight load ahead of the x loads
+    dma_x(xf, kbase + min(i + 2, nk - 1) * kTK);
     step(xs, cur);
-    MLORA_WAIT_VM(kWLoads + kXLoads + kWLoads);  // x(i + 1) has landed
-    lds_sync();
+    MLORA_WAIT_VM(kWLoads + kXLoads);  // x(i + 1) has landed
+    step_sync();
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
