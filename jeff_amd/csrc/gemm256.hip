@@ -1,8 +1,10 @@
 // Prefill-sized INT4 base product with the LoRA second factor fused (the same arithmetic as base.hip's kernels):
 //   y[perm[p], c] = bf16( sum_k x[perm[p], k] W[c, k] + sum_q mid[p, rho_j + q] sB_j[a][c - o_j, q] )
-// Tiles of 256 sorted tokens x 256 columns, 8 waves of 128 x 64 (2 x 4), 32x32x16 bf16 MFMA, float32 accumulators;
-// two waves per SIMD. The MFMAs take the weights as their first operand, so each lane's accumulators hold four
-// consecutive output columns of one token row.
+// Tiles of 256 sorted tokens x 256 columns, 8 waves of 256 x 32 (each wave all of the tile's rows and its own 32
+// columns), 32x32x16 bf16 MFMA, float32 accumulators; two waves per SIMD. The MFMAs take the weights as their first
+// operand, so each lane's accumulators hold four consecutive output columns of one token row. A wave owning its
+// columns alone dequantises each weight once per tile (8 MFMAs per dequantised word); the price is that every wave
+// reads all 256 rows of x from LDS.
 //
 // Per K step of 64 inputs:
 //  - x: the 256 gathered rows go straight from memory to LDS (buffer loads with the LDS flag, 16 bytes per lane, no
@@ -10,7 +12,7 @@
 //  - weights: no LDS at all. Each lane loads the packed words that form its own operands (one 32-bit word = the 8
 //    consecutive inputs of one column that a 32x32x16 operand lane holds), one step ahead, with the raw scale and
 //    zero point of its columns, and dequantises them to bf16((c - z) s) in registers, the next 16 inputs' words
-//    interleaved with the current MFMAs. The two waves sharing a column range both dequantise it.
+//    interleaved with the current MFMAs.
 // With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: a bare barrier after an
 // explicit wait for the x rows of the next step (a __syncthreads(), or any release fence, would also wait for the
 // rows two steps ahead).
@@ -33,7 +35,7 @@ constexpr int kTM = 256, kTN = 256, kTK = 64;
 constexpr int kThreads = 512;
 constexpr int kRankChunk = 64;   // ranks of sB staged per epilogue pass
 constexpr int kXLoads = 4;       // global_load_lds instructions per lane and step
-constexpr int kWLoads = 8 + 4;   // weight loads per lane and step: 2 x 4 words, 2 scales, 2 zero points
+constexpr int kWLoads = 4 + 2;   // weight loads per lane and step: 4 words, a scale, a zero point
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -75,11 +77,11 @@ __device__ __forceinline__ int xcd_tile(int b, int nb) {
   return xcd * per + min(xcd, extra) + slot;
 }
 
-// One step's weights as loaded by a lane: word [nb][k16] of each of its two 32-column blocks, and the raw bf16
-// scale and zero point of its two columns (converted only when used, a step later)
+// One step's weights as loaded by a lane: word [k16] of its column, and the raw bf16 scale and zero point of its
+// column (converted only when used, a step later)
 struct WStage {
-  uint32_t w[2][4];
-  uint32_t sbits[2], zbyte[2];
+  uint32_t w[4];
+  uint32_t sbits, zbyte;
 };
 
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
@@ -88,8 +90,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
                                                                const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec,
                                                                float* __restrict__ part, int32_t ksplit) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
   // Block b -> (K range ks, row tile mt, column tile nt), column tiles innermost: the blocks that share x rows (one
   // row tile and K range) are consecutive and so run on one XCD.
   const int b = xcd_tile(blockIdx.x, gridDim.x);
@@ -129,93 +131,72 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     const int64_t p = p0 + row;
     xoff[i] = (uint32_t)(((int64_t)r.tok_perm[p < T ? p : 0] * x_stride + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
   }
-  auto dma_x = [&](uint16_t* buf, int kc) {
+  auto dma_x = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(buf + (8 * i + wave) * 8 * kTK), 16, xoff[i], kc * 2,
                                                0, 0);
   };
 
-  // weights: lane l of block nb holds column n0 + 64 wn + 32 nb + (l & 31) and, for 16 inputs k16, the word of
-  // inputs 16 k16 + 8 (l >> 5) .. +7; columns past the layout read column 0 and get zero weights (scale 0)
-  bool colok[2];
-  uint32_t woff[2], soff[2], zoff[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int c = n0 + wn * 64 + nb * 32 + (lane & 31);
-    colok[nb] = c < w.columns;
-    const uint32_t gc = colok[nb] ? c : 0;
-    woff[nb] = (gc + (uint32_t)(lane >> 5) * w.columns) * 4;
-    soff[nb] = gc * 2;
-    zoff[nb] = asym ? gc : gc * 2;
-  }
+  // weights: lane l of wave w holds column n0 + 32 w + (l & 31) and, for 16 inputs k16, the word of inputs
+  // 16 k16 + 8 (l >> 5) .. +7; columns past the layout read column 0 and get zero weights (scale 0)
+  const int wcol = n0 + wave * 32 + (lane & 31);
+  const bool colok = wcol < w.columns;
+  const uint32_t gcol = colok ? wcol : 0;
+  const uint32_t woff = (gcol + (uint32_t)(lane >> 5) * w.columns) * 4;
+  const uint32_t soff = gcol * 2;
+  const uint32_t zoff = asym ? gcol : gcol * 2;
   const int wstep = w.columns * 8;  // bytes between the words of k16 and k16 + 1
-  auto fetch_w = [&](WStage& st, int kc) {
+  auto fetch_w = [&](WStage& st, int kc) __attribute__((always_inline)) {
     const int wbase = (kc / 8) * w.columns * 4;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int k16 = 0; k16 < 4; ++k16)
-        st.w[nb][k16] = __builtin_amdgcn_raw_buffer_load_b32(wres, woff[nb], wbase + k16 * wstep, 0);
+    for (int k16 = 0; k16 < 4; ++k16) st.w[k16] = __builtin_amdgcn_raw_buffer_load_b32(wres, woff, wbase + k16 * wstep, 0);
     const int g = (kc >> gshift) * w.columns;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      st.sbits[nb] = __builtin_amdgcn_raw_buffer_load_b16(sres, soff[nb], g * 2, 0);
-      st.zbyte[nb] = __builtin_amdgcn_raw_buffer_load_b8(zres, zoff[nb], asym ? g : g * 2, 0);
-    }
+    st.sbits = __builtin_amdgcn_raw_buffer_load_b16(sres, soff, g * 2, 0);
+    st.zbyte = __builtin_amdgcn_raw_buffer_load_b8(zres, zoff, asym ? g : g * 2, 0);
   };
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[8];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x16_t{};
+  for (int mb = 0; mb < 8; ++mb) acc[mb] = f32x16_t{};
 
   // (indexed as 16-byte elements of the buffer: each read's address is then one index into the LDS array, which
   // keeps the compiler's knowledge of which array it reads, so it does not wait for x loads into the other buffers)
-  auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[4]) {
+  auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[8]) {
     const int c = 2 * k16 + (lane >> 5);
     const uint4* xv = reinterpret_cast<const uint4*>(xs);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) a[mb] = xv[swz(wm * 128 + mb * 32 + (lane & 31), c) >> 3];
+    for (int mb = 0; mb < 8; ++mb) a[mb] = xv[swz(mb * 32 + (lane & 31), c) >> 3];
   };
   // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. The A
   // reads and the dequantisation of the next 16 inputs are interleaved with the current 16 inputs' MFMAs (one MFMA,
   // then a few VALU instructions or an LDS read), so the matrix core works while the wave converts.
-  auto step = [&](const uint16_t* xs, const WStage& ws) {
-    float sv[2], zs[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const float s0v = bf16_to_f32(ws.sbits[nb]);
-      const float zv = asym ? (float)ws.zbyte[nb] : 8.0f;
-      sv[nb] = colok[nb] ? s0v : 0.0f;
-      zs[nb] = colok[nb] ? zv * s0v : 0.0f;
-    }
-    uint4 a0[4], a1[4], b0[2], b1[2];
+  auto step = [&](const uint16_t* xs, const WStage& ws) __attribute__((always_inline)) {
+    const float s0v = bf16_to_f32(ws.sbits);
+    const float zv = asym ? (float)ws.zbyte : 8.0f;
+    const float sv = colok ? s0v : 0.0f;
+    const float zs = colok ? zv * s0v : 0.0f;
+    uint4 a0[8], a1[8], b0, b1;
     load_a(xs, 0, a0);
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) b0[nb] = dequant_word(ws.w[nb][0], sv[nb], zs[nb]);
+    b0 = dequant_word(ws.w[0], sv, zs);
 #pragma unroll
     for (int k16 = 0; k16 < kTK / 16; ++k16) {
-      uint4 (&ca)[4] = (k16 & 1) ? a1 : a0;
-      uint4 (&na)[4] = (k16 & 1) ? a0 : a1;
-      uint4 (&cb)[2] = (k16 & 1) ? b1 : b0;
-      uint4 (&nbv)[2] = (k16 & 1) ? b0 : b1;
+      uint4 (&ca)[8] = (k16 & 1) ? a1 : a0;
+      uint4 (&na)[8] = (k16 & 1) ? a0 : a1;
+      uint4& cb = (k16 & 1) ? b1 : b0;
+      uint4& nbv = (k16 & 1) ? b0 : b1;
       if (k16 + 1 < kTK / 16) {
         load_a(xs, k16 + 1, na);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) nbv[nb] = dequant_word(ws.w[nb][k16 + 1], sv[nb], zs[nb]);
+        nbv = dequant_word(ws.w[k16 + 1], sv, zs);
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(cb[nb], ca[mb], acc[mb][nb]);
+      for (int mb = 0; mb < 8; ++mb) acc[mb] = mfma32(cb, ca[mb], acc[mb]);
       if (k16 + 1 < kTK / 16) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
-          if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
         }
       }
     }
@@ -271,18 +252,16 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     // second launch adds the ranges in order, the LoRA term and rounds. Lane l holds four consecutive columns.
     float* pk = part + (int64_t)ks * T * w.columns;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int64_t p = p0 + wm * 128 + mb * 32 + (lane & 31);
+    for (int mb = 0; mb < 8; ++mb) {
+      const int64_t p = p0 + mb * 32 + (lane & 31);
       if (p >= T) continue;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c = n0 + wn * 64 + nb * 32 + g * 8 + (lane >> 5) * 4;
-          if (c >= w.columns) continue;
-          *reinterpret_cast<float4*>(pk + p * w.columns + c) =
-              make_float4(acc[mb][nb][4 * g], acc[mb][nb][4 * g + 1], acc[mb][nb][4 * g + 2], acc[mb][nb][4 * g + 3]);
-        }
+      for (int g = 0; g < 4; ++g) {
+        const int c = n0 + wave * 32 + g * 8 + (lane >> 5) * 4;
+        if (c >= w.columns) continue;
+        *reinterpret_cast<float4*>(pk + p * w.columns + c) =
+            make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+      }
     }
     return;
   }
@@ -299,15 +278,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     const int jlo = matrix_of(L, n0), jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
     for (int j = jlo; j <= jhi; ++j) {
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
-      // columns of the wave's two blocks inside matrix j (others get zero operands)
-      bool cin[2];
-      int64_t boff[2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int cc = n0 + wn * 64 + nb * 32 + (lane & 31);
-        cin[nb] = cc >= oj && cc < oj + cj && cc < n_out;
-        boff[nb] = L.off_b[j] + (int64_t)((cin[nb] ? cc : oj) - oj) * capj;
-      }
+      // the wave's column inside matrix j (others get zero operands)
+      const int cc = n0 + wave * 32 + (lane & 31);
+      const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
+      const int64_t boff = L.off_b[j] + (int64_t)((cin ? cc : oj) - oj) * capj;
       for (int rc = 0; rc < capj; rc += kRankChunk) {
         // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
         lds_sync();  // every wave is done with the previous chunk's rows
@@ -320,48 +294,42 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                    0);
         }
         // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
-        auto load_b = [&](int s, uint4 (&bv)[2][4], int& rk) {
+        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) {
           const int a = r.seg_adapter[s];
           rk = a == 0 ? 0 : min(live_rank(L, a, j) - rc, kRankChunk);
           const uint16_t* prow = L.pool + (int64_t)a * L.pool_stride;
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-            for (int k16 = 0; k16 < 4; ++k16) {
-              const int kk = 16 * k16 + 8 * (lane >> 5);
-              const int q = min(rc + kk, capj - 8);
-              bv[nb][k16] = *reinterpret_cast<const uint4*>(prow + boff[nb] + q);
-            }
+          for (int k16 = 0; k16 < 4; ++k16) {
+            const int kk = 16 * k16 + 8 * (lane >> 5);
+            const int q = min(rc + kk, capj - 8);
+            bv[k16] = *reinterpret_cast<const uint4*>(prow + boff + q);
+          }
         };
-        auto apply = [&](int s, uint4 (&bv)[2][4], int rk) {
+        auto apply = [&](int s, uint4 (&bv)[4], int rk) {
           if (rk <= 0) return;
           const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb)
+          for (int k16 = 0; k16 < 4; ++k16)
+            bv[k16] = cin ? keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-            for (int k16 = 0; k16 < 4; ++k16)
-              bv[nb][k16] = cin[nb] ? keep_first(bv[nb][k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            const int64_t r0 = p0 + wm * 128 + mb * 32;
+          for (int mb = 0; mb < 8; ++mb) {
+            const int64_t r0 = p0 + mb * 32;
             if (r0 >= se || r0 + 32 <= sb) continue;
             const int64_t row = r0 + (lane & 31);
             const bool rin = row >= sb && row < se;
 #pragma unroll
             for (int k16 = 0; k16 < 4; ++k16) {
               if (16 * k16 >= rk) break;
-              uint4 av = *reinterpret_cast<const uint4*>(
-                  &g_x0[swz(wm * 128 + mb * 32 + (lane & 31), 2 * k16 + (lane >> 5))]);
+              uint4 av = reinterpret_cast<const uint4*>(g_x0)[swz(mb * 32 + (lane & 31), 2 * k16 + (lane >> 5)) >> 3];
               av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-              for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(bv[nb][k16], av, acc[mb][nb]);
+              acc[mb] = mfma32(bv[k16], av, acc[mb]);
             }
           }
         };
-        uint4 b0[2][4], b1[2][4];
+        uint4 b0[4], b1[4];
         int rk0, rk1;
         load_b(s_lo, b0, rk0);
-        MLORA_WAIT_VM(8);  // the first factors have landed (the 8 sB loads may still be in flight)
+        MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
         lds_sync();
         for (int s = s_lo; s <= s_hi; s += 2) {
           load_b(min(s + 1, s_hi), b1, rk1);
@@ -374,29 +342,27 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     }
   }
 
-  // Single rounding to bf16 and the stores, through LDS one half of the tile (128 rows, one wave row) at a time:
-  // lane l holds, for row mb * 32 + (l & 31) of its wave's rows, the four consecutive columns 8 g + 4 (l >> 5) .. +3
-  // of each 32-column block; it writes them to LDS (columns 0..127 of the tile in g_x0, 128..255 in g_x1, 256-byte
-  // rows with their 16-byte chunks XOR-swizzled by (row & 15)), then every thread reads 16-byte chunks back and
-  // writes whole 512-byte tile rows to the token's output row (and to its request's last-token row).
+  // Single rounding to bf16 and the stores, through LDS one half of the tile (128 rows) at a time: lane l holds, for
+  // row mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave
+  // writes its half-tile rows to LDS (columns 0..127 of the tile in g_x0, 128..255 in g_x1, 256-byte rows with their
+  // 16-byte chunks XOR-swizzled by (row & 15)), then every thread reads 16-byte chunks back and writes whole 512-byte
+  // tile rows to the token's output row (and to its request's last-token row).
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     lds_sync();  // every wave is done reading LDS
-    if (wm == half) {
-      uint16_t* buf = (wn >> 1) ? g_x1 : g_x0;
+    {
+      uint16_t* buf = (wave >> 2) ? g_x1 : g_x0;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int row = mb * 32 + (lane & 31);
-            const int col = (wn & 1) * 64 + nb * 32 + g * 8 + (lane >> 5) * 4;
-            const uint32_t lo = pack_bf16x2(acc[mb][nb][4 * g], acc[mb][nb][4 * g + 1]);
-            const uint32_t hi = pack_bf16x2(acc[mb][nb][4 * g + 2], acc[mb][nb][4 * g + 3]);
-            *reinterpret_cast<uint2*>(&buf[row * 128 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)]) =
-                make_uint2(lo, hi);
-          }
+        for (int g = 0; g < 4; ++g) {
+          const int mb = half * 4 + mq;
+          const int row = mq * 32 + (lane & 31);
+          const int col = (wave & 3) * 32 + g * 8 + (lane >> 5) * 4;
+          const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
+          const uint32_t hi = pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+          *reinterpret_cast<uint2*>(&buf[row * 128 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)]) = make_uint2(lo, hi);
+        }
     }
     lds_sync();
 #pragma unroll
