@@ -87,6 +87,7 @@ def main() -> int:
     from jeff_amd.fast_path import DT, Workspace
     from jeff_amd.int4_kernels import base_expand, int4_product, shrink
     from jeff_amd.int4_tiles import int4_tiles
+    from jeff_amd.epilogues import add_rms, silu_mul
     from jeff_amd.readout import readout_rows
 
     dev = torch.device("cuda:0")
@@ -224,6 +225,41 @@ def main() -> int:
                 "options": int(r["readout_pool"].shape[1]), "dim": int(r["readout_pool"].shape[2])}
         del hgraph
 
+    # the element-wise steps around the linear at this pass's shapes: residual add + RMSNorm of the hidden rows before
+    # the gate_up product, SiLU(gate) * up after it; each timed alone as above
+    gl = w.layers[0]["gate_up"]
+    hid, inter = gl.k, gl.out // 2
+    eg = torch.Generator(device="cuda").manual_seed(77)
+    ex = torch.randn(w.tokens, hid, device=dev, generator=eg).to(DT)
+    ed = torch.randn(w.tokens, hid, device=dev, generator=eg).to(DT)
+    ew = (1 + 0.1 * torch.randn(hid, device=dev, generator=eg)).float()
+    egu = torch.randn(w.tokens, 2 * inter, device=dev, generator=eg).to(DT)
+
+    def timed(fn, nbytes: float) -> dict:
+        reps = 20
+        g = torch.cuda.CUDAGraph()
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(3):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) / reps)
+        ms = statistics.median(ts)
+        return {"ms": ms, "bytes": nbytes, "hbm_frac": nbytes / (ms / 1e3) / PEAK_HBM}
+
+    epilogues = {"rows": w.tokens, "hidden": hid, "inter": inter,
+                 "add_rms": timed(lambda: add_rms(ex, ed, ew), 2.0 * w.tokens * hid * 4 + 4.0 * hid),
+                 "silu_mul": timed(lambda: silu_mul(egu), 2.0 * w.tokens * inter * 3)}
+    del ex, ed, egu
+
     cpu = None if args.no_cpu else cpu_baseline(w, xs, per_layer_acts, args.cpu_seconds)
     del graph, kgraph
     config = {"workload": args.workload, "tokens": w.tokens, "requests": w.requests, "layers": len(w.layers),
@@ -232,6 +268,7 @@ def main() -> int:
               "group_size": 128, "zero_points": True, "step_roofline": step_roof}
     if head is not None:
         config["decision_head"] = head
+    config["epilogues"] = epilogues
     print(json.dumps({"metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
                       "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
                       "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded; random INT4 weights and "

@@ -20,6 +20,8 @@
  *   mlora_int4_partials_bytes  Workspace.P sizing (split partial products)  int4_kernels.py:150-166
  *   mlora_readout_logits  readout_logits (per-adapter readout)          batched_kernels.py:492-504,522-536
  *   mlora_option_softmax  option_softmax (mask, temperature, softmax)     batched_kernels.py:507-519,539-553
+ *   mlora_add_rms      add_rms / rms (residual add + RMSNorm)              fast_path.py:80-100,295-298
+ *   mlora_silu_mul     silu_mul (SiLU of the gate half times the up half)  fast_path.py:141-156
  */
 #ifndef JEFF_MLORA_H
 #define JEFF_MLORA_H
@@ -37,6 +39,7 @@ extern "C" {
 #define MLORA_MAX_POOL_ROWS 262144  /* adapter pool rows (row 0 = the base, no update) */
 #define MLORA_READOUT_MAX_DIM 2048  /* hidden size of the decision head's readout */
 #define MLORA_READOUT_MAX_OPTIONS 256  /* answer options per readout */
+#define MLORA_EPILOGUE_MAX_N 8192   /* row length of add_rms */
 
 enum {
   MLORA_OK = 0,
@@ -167,6 +170,20 @@ int mlora_readout_logits(const uint16_t* hidden, int64_t hidden_stride, int32_t 
  * of (o < counts[b] ? logits[b][o] : -1e9) / temp_pool[adapters[b]]; temp_pool float32 (pool_rows). */
 int mlora_option_softmax(const float* logits, int32_t options, const int32_t* adapters, const int32_t* counts,
                          const float* temp_pool, int32_t pool_rows, int32_t rows, float* probs, void* stream);
+
+/* Residual add and RMSNorm of each of `rows` rows of n bf16 values (the reference's add_rms, and rms when d is NULL):
+ * x' = bf16(x + d) (written to xo when d is given; xo may be x), h = bf16(x' * rsqrt(sum(x'^2) / n + eps) * w1), the
+ * sum of squares in float32 in a fixed order. w1 float32 (n) = 1 + the norm's weight. n a multiple of 8, at most
+ * MLORA_EPILOGUE_MAX_N; rows, w1 16-byte aligned, strides multiples of 8 elements. */
+int mlora_add_rms(const uint16_t* x, int64_t x_stride, const uint16_t* d, int64_t d_stride, const float* w1,
+                  uint16_t* xo, int64_t xo_stride, uint16_t* h, int64_t h_stride, int64_t rows, int32_t n, float eps,
+                  void* stream);
+
+/* The gated activation after the gate_up product (the reference's silu_mul): for each of `rows` rows of gu (the
+ * gate half in columns 0..inter-1, the up half in inter..2 inter-1), y = bf16(bf16(g / (1 + exp(-g))) * u). inter a
+ * multiple of 8; rows 16-byte aligned, strides multiples of 8 elements. */
+int mlora_silu_mul(const uint16_t* gu, int64_t gu_stride, uint16_t* y, int64_t y_stride, int64_t rows, int32_t inter,
+                   void* stream);
 
 #ifdef __cplusplus
 }

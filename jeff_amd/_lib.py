@@ -15,6 +15,7 @@ MAX_REQUESTS = 8192
 MAX_POOL_ROWS = 262144
 READOUT_MAX_DIM = 2048
 READOUT_MAX_OPTIONS = 256
+EPILOGUE_MAX_N = 8192
 
 OK, EINVAL, EALIGN, EOVERFLOW, EWORKSPACE, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3, -4, -5, -6
 ERRORS = {EINVAL: "invalid argument (a null pointer, a bad size or shape)",
@@ -30,7 +31,7 @@ FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_GEMV, FORCE_SHRINK_MFMA, FORCE_BA
 
 EXPORTS = ("mlora_abi_version", "mlora_workspace_bytes", "mlora_int4_partials_bytes", "mlora_route", "mlora_dequant",
            "mlora_shrink", "mlora_int4_linear", "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits",
-           "mlora_option_softmax")
+           "mlora_option_softmax", "mlora_add_rms", "mlora_silu_mul")
 
 c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -96,6 +97,11 @@ def lib() -> ctypes.CDLL:
         h.mlora_readout_logits.argtypes = [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_vp, c_i32, c_vp, c_vp]
         h.mlora_option_softmax.restype = c_i32
         h.mlora_option_softmax.argtypes = [c_vp, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp]
+        h.mlora_add_rms.restype = c_i32
+        h.mlora_add_rms.argtypes = [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i32,
+                                    ctypes.c_float, c_vp]
+        h.mlora_silu_mul.restype = c_i32
+        h.mlora_silu_mul.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp]
         h.mlora_int4_partials_bytes.restype = ctypes.c_size_t
         h.mlora_int4_partials_bytes.argtypes = [P(Int4), P(Lora), P(Route), c_i32]
         h.mlora_lora_add.restype = c_i32

@@ -305,5 +305,30 @@ int mlora_option_softmax(const float* logits, int32_t options, const int32_t* ad
                                static_cast<hipStream_t>(stream));
 }
 
+int mlora_add_rms(const uint16_t* x, int64_t x_stride, const uint16_t* d, int64_t d_stride, const float* w1,
+                  uint16_t* xo, int64_t xo_stride, uint16_t* h, int64_t h_stride, int64_t rows, int32_t n, float eps,
+                  void* stream) {
+  if (rows < 0 || n <= 0 || !(eps >= 0.0f)) return MLORA_EINVAL;
+  if (n % 8 || n > MLORA_EPILOGUE_MAX_N) return MLORA_EUNSUPPORTED;
+  if (rows == 0) return MLORA_OK;
+  if (x == nullptr || w1 == nullptr || h == nullptr || (d != nullptr && xo == nullptr)) return MLORA_EINVAL;
+  if (x_stride < n || h_stride < n || (d != nullptr && (d_stride < n || xo_stride < n))) return MLORA_EINVAL;
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(h) || x_stride % 8 || h_stride % 8) return MLORA_EALIGN;
+  if (d != nullptr && (!aligned16(d) || !aligned16(xo) || d_stride % 8 || xo_stride % 8)) return MLORA_EALIGN;
+  return launch_add_rms(x, x_stride, d, d_stride, w1, xo, xo_stride, h, h_stride, rows, n, eps,
+                        static_cast<hipStream_t>(stream));
+}
+
+int mlora_silu_mul(const uint16_t* gu, int64_t gu_stride, uint16_t* y, int64_t y_stride, int64_t rows, int32_t inter,
+                   void* stream) {
+  if (rows < 0 || inter <= 0) return MLORA_EINVAL;
+  if (inter % 8) return MLORA_EUNSUPPORTED;
+  if (rows == 0) return MLORA_OK;
+  if (gu == nullptr || y == nullptr || gu_stride < 2 * (int64_t)inter || y_stride < inter) return MLORA_EINVAL;
+  if (!aligned16(gu) || !aligned16(y) || gu_stride % 8 || y_stride % 8) return MLORA_EALIGN;
+  if (rows * (int64_t)(inter / 8) >= ((int64_t)1 << 31) * 256) return MLORA_EOVERFLOW;
+  return launch_silu_mul(gu, gu_stride, y, y_stride, rows, inter, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
 #pragma GCC visibility pop

@@ -129,6 +129,12 @@ int launch_readout_logits(const uint16_t* hidden, int64_t hidden_stride, int32_t
                           int32_t rows, float* logits, hipStream_t stream);
 int launch_option_softmax(const float* logits, int32_t options, const int32_t* adapters, const int32_t* counts,
                           const float* temp_pool, int32_t pool_rows, int32_t rows, float* probs, hipStream_t stream);
+// The element-wise work around the linear: residual add + RMSNorm; SiLU of the gate half times the up half.
+int launch_add_rms(const uint16_t* x, int64_t x_stride, const uint16_t* d, int64_t d_stride, const float* w1,
+                   uint16_t* xo, int64_t xo_stride, uint16_t* h, int64_t h_stride, int64_t rows, int32_t n, float eps,
+                   hipStream_t stream);
+int launch_silu_mul(const uint16_t* gu, int64_t gu_stride, uint16_t* y, int64_t y_stride, int64_t rows, int32_t inter,
+                    hipStream_t stream);
 // The split product's second launch stages its rows' first factors in LDS: at most this stacked rank.
 #define MLORA_SPLIT_MAX_RANK 512
 

@@ -13,6 +13,7 @@ Modules (each function cites the reference file:line it restates; paths are rela
              `engine/fast_path.py:167,189`).
 - `readout`: the decision head, per-adapter readout logits rounded to bfloat16 and the masked, tempered softmax
              (`engine/batched_kernels.py:492-559`).
+- `epilogue`: residual add + RMSNorm and SiLU(gate) * up around the linear (`engine/fast_path.py:80-156,295-298`).
 - `layer`:   the reference's torch layer `LoraLinear.forward` applied per adapter segment (`engine/lora.py:204-220`)
              in "model" and "float32" precision; the float64 exact result and the forward error bounds of
              `tests/test_int4_kernels_cuda.py:108-168`.
@@ -27,6 +28,9 @@ How each function is pinned (checked by `tests/test_oracle_*.py` against golden 
 - routing: invariants (bijection, stable order, one adapter per segment, coverage) and equality with
   `adp[t // row_len]` on uniform rows, brute force on tiny inputs.
 - layer: the float64 exact result against an independent per-element sum; the bound model is the reference's own.
+- epilogue: x + d bit for bit against torch's float32 addition; the norm against the reference's standard-path
+  formula in torch float32 (`rms`, `engine/fast_path.py:295-298`) and closed forms (a constant row, a zero row), planted
+  mistakes (no eps, a mean over n - 1, no w1); SiLU against torch's float64 silu and its limits.
 - readout: logits against a per-element sum in exact rationals on small inputs (and so the rounding through float32
   to bfloat16 on every value), planted mistakes (another adapter's readout, a transposed readout); the softmax against
   closed forms (one option kept gives 1, equal logits give 1/count, a temperature t equals logits divided by t at

@@ -40,6 +40,7 @@ def test_header_constants_match_the_binding() -> None:
     assert const("MLORA_MAX_POOL_ROWS") == _lib.MAX_POOL_ROWS
     assert const("MLORA_READOUT_MAX_DIM") == _lib.READOUT_MAX_DIM
     assert const("MLORA_READOUT_MAX_OPTIONS") == _lib.READOUT_MAX_OPTIONS
+    assert const("MLORA_EPILOGUE_MAX_N") == _lib.EPILOGUE_MAX_N
     assert const("MLORA_ROUTE_BAD_ADAPTER") == _lib.ROUTE_BAD_ADAPTER
     assert const("MLORA_ROUTE_BAD_SEQLENS") == _lib.ROUTE_BAD_SEQLENS
     for name, value in (("MLORA_FORCE_BASE_GEMV", _lib.FORCE_BASE_GEMV), ("MLORA_FORCE_BASE_MFMA", _lib.FORCE_BASE_MFMA),
