@@ -2,8 +2,9 @@
 // token position p of an adapter segment, matrix j of the group and live rank q. Summed in float32 in a fixed
 // order and rounded once to bf16, as the reference rounds its first factor before the second product
 // (engine/fast_path.py:159-177,196; engine/int4_kernels.py:67-82,120). Two kernels, chosen by segment length:
-//  - shrink_gemv: few tokens per adapter (decode). One workgroup per (segment, matrix, 16 ranks) streams those 16
-//    rows of A once, coalesced, and reduces across the workgroup in a fixed order. Memory-bound on A.
+//  - shrink_seg: few tokens per adapter (decode). One workgroup per (segment, 32-rank block) streams those 32 rows
+//    of A once into MFMA operands, the segment's rows as the other operand; its waves split the inputs and add their
+//    sums in a fixed order. Memory-bound on A.
 //  - shrink_mfma: long segments (prefill). One workgroup per 32 sorted positions; its waves split the inputs, stream
 //    the x rows through per-wave LDS rings and A into registers one chunk ahead, and add their partial sums in a
 //    fixed order.
@@ -12,75 +13,6 @@
 namespace {
 
 using namespace mlora;
-
-constexpr int kGemvThreads = 256;
-constexpr int kGemvRows = 4;    // tokens per pass over A
-constexpr int kGemvRanks = 16;  // rank rows of A per workgroup
-
-__global__ __launch_bounds__(kGemvThreads) void shrink_gemv_kernel(mlora_lora_t L, mlora_route_t r,
-                                                                  const uint16_t* __restrict__ x, int64_t x_stride,
-                                                                  int32_t k, uint16_t* __restrict__ mid,
-                                                                  int32_t qchunks) {
-  __shared__ float red[kGemvThreads / kWave][kWave];
-  const int per_seg = L.n_mats * qchunks;
-  const int s = blockIdx.x / per_seg;
-  const int rem = blockIdx.x - s * per_seg;
-  const int j = rem / qchunks, qc = rem - j * qchunks;
-  if (s >= *r.num_segs) return;
-  const int a = r.seg_adapter[s];
-  const int rank = live_rank(L, a, j);
-  const int q0 = qc * kGemvRanks;
-  if (q0 >= rank) return;
-  const int nq = min(kGemvRanks, rank - q0);
-  const int rho = rank_offset(L, j);
-  const int p_begin = r.seg_start[s], p_end = r.seg_start[s + 1];
-  const uint16_t* A = L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rho + q0) * k;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kw = k / 8;
-  for (int pc = p_begin; pc < p_end; pc += kGemvRows) {
-    const int rows = min(kGemvRows, p_end - pc);
-    const uint16_t* xr[kGemvRows];
-#pragma unroll
-    for (int rr = 0; rr < kGemvRows; ++rr)  // rows past the segment repeat its last row; their sums are dropped
-      xr[rr] = x + (int64_t)r.tok_perm[pc + min(rr, rows - 1)] * x_stride;
-    float v[kGemvRows * kGemvRanks];
-#pragma unroll
-    for (int i = 0; i < kGemvRows * kGemvRanks; ++i) v[i] = 0.0f;
-    for (int i = tid; i < kw; i += kGemvThreads) {
-      // every load is issued before any use (rank rows past the live rank re-read the last live row and are dropped),
-      // so the 4 + 16 requests of a thread are in flight together
-      uint4 xv[kGemvRows], av[kGemvRanks];
-#pragma unroll
-      for (int rr = 0; rr < kGemvRows; ++rr) xv[rr] = *reinterpret_cast<const uint4*>(xr[rr] + 8 * i);
-#pragma unroll
-      for (int q = 0; q < kGemvRanks; ++q)
-        av[q] = *reinterpret_cast<const uint4*>(A + (int64_t)min(q, nq - 1) * k + 8 * i);
-#pragma unroll
-      for (int q = 0; q < kGemvRanks; ++q)
-#pragma unroll
-        for (int rr = 0; rr < kGemvRows; ++rr) v[rr * kGemvRanks + q] = dot8(xv[rr], av[q], v[rr * kGemvRanks + q]);
-    }
-    // reduce-scatter across the wave: afterwards lane l holds the wave's sum of value l (row l/16, rank l%16)
-#pragma unroll
-    for (int h = 32; h >= 1; h >>= 1) {
-      const bool upper = (lane & h) != 0;
-#pragma unroll
-      for (int i = 0; i < h; ++i) {
-        const float send = upper ? v[i] : v[i + h];
-        const float keep = upper ? v[i + h] : v[i];
-        v[i] = keep + __shfl_xor(send, h);
-      }
-    }
-    red[wave][lane] = v[0];
-    __syncthreads();
-    if (wave == 0) {
-      const float sum = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-      const int rr = lane / kGemvRanks, q = lane % kGemvRanks;
-      if (rr < rows && q < nq) mid[(int64_t)(pc + rr) * L.rank_cap + rho + q0 + q] = f32_to_bf16(sum);
-    }
-    __syncthreads();
-  }
-}
 
 // The (matrix, 32-rank block) of block index b of an adapter whose live ranks are rk[].
 __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int& j, int& kb) {
@@ -240,6 +172,92 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
   }
 }
 
+constexpr int kDWaves = 8;   // waves per workgroup of the segment form, each a contiguous share of the inputs
+constexpr int kDUnroll = 8;  // 16-input steps a wave has in flight
+
+// Short segments (decode): one workgroup per (segment, 32-rank block of the adapter's live ranks). Its 8 waves split
+// the input dimension; a lane streams its rank row of A and its token row of x (the segment's rows as the second
+// MFMA operand, rows past the segment masked to zero) straight into MFMA operands, 8 steps of 16 inputs in flight;
+// one 32x32x16 MFMA per step accumulates a 32-rank x 32-row block. The waves' sums are added in wave order through
+// LDS and rounded once. Segments longer than 32 rows take their rows 32 at a time (A is then re-read from L2).
+__global__ __launch_bounds__(kDWaves * 64) void shrink_seg_kernel(mlora_lora_t L, mlora_route_t r,
+                                                                 const uint16_t* __restrict__ x, int64_t x_stride,
+                                                                 int32_t k, uint16_t* __restrict__ mid,
+                                                                 int32_t max_blocks) {
+  __shared__ float red[kDWaves * 16 * kWave];
+  const int s = blockIdx.x / max_blocks, b = blockIdx.x - s * max_blocks;
+  if (s >= *r.num_segs) return;
+  const int a = r.seg_adapter[s];
+  if (a == 0) return;  // the base row: no first factor is read
+  int rk[MLORA_MAX_MATS];
+  int nblk = 0;
+  for (int j = 0; j < L.n_mats; ++j) {
+    rk[j] = live_rank(L, a, j);
+    nblk += (rk[j] + 31) >> 5;
+  }
+  if (b >= nblk) return;
+  int j = 0, kb = 0;
+  rank_block(rk, L.n_mats, b, j, kb);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = kb * 32 + (lane & 31);  // this lane's rank row
+  const bool aok = n < rk[j];
+  const uint32_t amask = aok ? 0xFFFFFFFFu : 0u;
+  const uint16_t* arow =
+      L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rank_offset(L, j) + (aok ? n : 0)) * k + 8 * (lane >> 5);
+  const int steps = k / 16;
+  const int c0 = (wave * steps) / kDWaves, c1 = ((wave + 1) * steps) / kDWaves;  // this wave's 16-input steps
+  const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+  for (int64_t p0 = sb; p0 < se; p0 += 32) {
+    const int64_t prow = p0 + (lane & 31);
+    const bool rin = prow < se;
+    const uint32_t xmask = rin ? 0xFFFFFFFFu : 0u;
+    const uint16_t* xrow = x + (int64_t)r.tok_perm[rin ? prow : p0] * x_stride + 8 * (lane >> 5);
+    f32x16_t acc = f32x16_t{};
+    // every load is unconditional (steps past the wave's range re-read its last one and are not multiplied)
+    uint4 av[2][kDUnroll], xv[2][kDUnroll];
+    auto issue = [&](uint4 (&aq)[kDUnroll], uint4 (&xq)[kDUnroll], int c) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kDUnroll; ++u) {
+        const int kk = max(min(c + u, c1 - 1), c0) * 16;
+        aq[u] = *reinterpret_cast<const uint4*>(arow + kk);
+        xq[u] = *reinterpret_cast<const uint4*>(xrow + kk);
+      }
+    };
+    auto compute = [&](const uint4 (&aq)[kDUnroll], const uint4 (&xq)[kDUnroll], int c) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kDUnroll; ++u) {
+        if (c + u >= c1) break;
+        const uint4 am = make_uint4(aq[u].x & amask, aq[u].y & amask, aq[u].z & amask, aq[u].w & amask);
+        const uint4 xm = make_uint4(xq[u].x & xmask, xq[u].y & xmask, xq[u].z & xmask, xq[u].w & xmask);
+        acc = mfma32(am, xm, acc);
+      }
+    };
+    if (c1 > c0) {
+      issue(av[0], xv[0], c0);
+      for (int c = c0; c < c1; c += 2 * kDUnroll) {
+        issue(av[1], xv[1], c + kDUnroll);
+        compute(av[0], xv[0], c);
+        if (c + kDUnroll >= c1) break;
+        issue(av[0], xv[0], c + 2 * kDUnroll);
+        compute(av[1], xv[1], c + kDUnroll);
+      }
+    }
+    __syncthreads();  // the previous row block's sums are read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc[i];
+    __syncthreads();
+    for (int e = tid; e < 16 * kWave; e += kDWaves * kWave) {
+      const int i = e / kWave, ln = e % kWave;
+      float sum = red[i * kWave + ln];
+#pragma unroll
+      for (int w = 1; w < kDWaves; ++w) sum += red[(w * 16 + i) * kWave + ln];
+      const int q = kb * 32 + (i >> 2) * 8 + (ln >> 5) * 4 + (i & 3);
+      const int64_t p = p0 + (ln & 31);
+      if (q < rk[j] && p < se) mid[p * L.rank_cap + rank_offset(L, j) + q] = f32_to_bf16(sum);
+    }
+  }
+}
+
 }  // namespace
 
 int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x, int64_t x_stride, int32_t k,
@@ -250,13 +268,12 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
     hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks), dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k,
                        mid);
   } else {
-    int maxcap = 0;
-    for (int j = 0; j < L.n_mats; ++j) maxcap = L.cap[j] > maxcap ? L.cap[j] : maxcap;
-    const int qchunks = (maxcap + kGemvRanks - 1) / kGemvRanks;
-    const int64_t blocks = (int64_t)r.max_segs * L.n_mats * qchunks;
+    int max_blocks = 0;  // 32-rank blocks of an adapter using every matrix's capacity
+    for (int j = 0; j < L.n_mats; ++j) max_blocks += (L.cap[j] + 31) / 32;
+    const int64_t blocks = (int64_t)r.max_segs * max_blocks;
     if (blocks == 0) return MLORA_OK;
-    hipLaunchKernelGGL(shrink_gemv_kernel, dim3((unsigned)blocks), dim3(kGemvThreads), 0, stream, L, r, x, x_stride,
-                       k, mid, qchunks);
+    hipLaunchKernelGGL(shrink_seg_kernel, dim3((unsigned)blocks), dim3(kDWaves * 64), 0, stream, L, r, x, x_stride, k,
+                       mid, max_blocks);
   }
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }
