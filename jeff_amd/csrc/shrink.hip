@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
 }
 
 constexpr int kDWaves = 8;   // waves per workgroup of the segment form, each a contiguous share of the inputs
-constexpr int kDUnroll = 8;  // 16-input steps a wave has in flight
+constexpr int kDUnroll = 4;  // 16-input steps per load batch; two batches in flight (120 VGPRs: two workgroups per CU)
 
 // Short segments (decode): one workgroup per (segment, 32-rank block of the adapter's live ranks). Its 8 waves split
 // the input dimension; a lane streams its rank row of A and its token row of x (the segment's rows as the second
