@@ -84,6 +84,8 @@ struct WStage {
   uint32_t sbits, zbyte;
 };
 
+// MB: 32-row blocks of a tile (8: 256 rows; 7: 224 rows, chosen by the host when it takes fewer rounds of tiles)
+template <int MB>
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
@@ -98,7 +100,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   const int t = b % (gridDim.x / ksplit), ks = b / (gridDim.x / ksplit);
   const int mt = t / n_tiles, nt = t - mt * n_tiles;
   const int64_t T = r.tokens;
-  const int64_t p0 = (int64_t)mt * kTM;
+  constexpr int kRows = 32 * MB;  // the tile's rows (LDS buffers hold 256; rows past kRows are loaded, never used)
+  const int64_t p0 = (int64_t)mt * kRows;
   const int n0 = nt * kTN;
 
   // Loads go through buffer resources: the per-lane byte offsets below stay fixed for the whole K loop and the K
@@ -121,8 +124,9 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // +(l >> 3), which holds logical chunk (l & 7) ^ (l >> 3). Rows past the tokens read row 0 of the pass.
   if (tid < kTM) {
     const int64_t p = p0 + tid;
-    g_orig[tid] = p < T ? r.tok_perm[p] : -1;
-    g_last[tid] = (p < T && last_out != nullptr) ? r.last_of[p] : -1;
+    const bool mine = tid < kRows && p < T;
+    g_orig[tid] = mine ? r.tok_perm[p] : -1;
+    g_last[tid] = (mine && last_out != nullptr) ? r.last_of[p] : -1;
   }
   uint32_t xoff[kXLoads];
 #pragma unroll
@@ -156,17 +160,17 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     st.zbyte = __builtin_amdgcn_raw_buffer_load_b8(zres, zoff, asym ? g : g * 2, 0);
   };
 
-  f32x16_t acc[8];
+  f32x16_t acc[MB];
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) acc[mb] = f32x16_t{};
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16_t{};
 
   // (indexed as 16-byte elements of the buffer: each read's address is then one index into the LDS array, which
   // keeps the compiler's knowledge of which array it reads, so it does not wait for x loads into the other buffers)
-  auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[8]) {
+  auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[MB]) __attribute__((always_inline)) {
     const int c = 2 * k16 + (lane >> 5);
     const uint4* xv = reinterpret_cast<const uint4*>(xs);
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) a[mb] = xv[swz(mb * 32 + (lane & 31), c) >> 3];
+    for (int mb = 0; mb < MB; ++mb) a[mb] = xv[swz(mb * 32 + (lane & 31), c) >> 3];
   };
   // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. The A
   // reads and the dequantisation of the next 16 inputs are interleaved with the current 16 inputs' MFMAs (one MFMA,
@@ -176,13 +180,13 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     const float zv = asym ? (float)ws.zbyte : 8.0f;
     const float sv = colok ? s0v : 0.0f;
     const float zs = colok ? zv * s0v : 0.0f;
-    uint4 a0[8], a1[8], b0, b1;
+    uint4 a0[MB], a1[MB], b0, b1;
     load_a(xs, 0, a0);
     b0 = dequant_word(ws.w[0], sv, zs);
 #pragma unroll
     for (int k16 = 0; k16 < kTK / 16; ++k16) {
-      uint4 (&ca)[8] = (k16 & 1) ? a1 : a0;
-      uint4 (&na)[8] = (k16 & 1) ? a0 : a1;
+      uint4 (&ca)[MB] = (k16 & 1) ? a1 : a0;
+      uint4 (&na)[MB] = (k16 & 1) ? a0 : a1;
       uint4& cb = (k16 & 1) ? b1 : b0;
       uint4& nbv = (k16 & 1) ? b0 : b1;
       if (k16 + 1 < kTK / 16) {
@@ -190,10 +194,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         nbv = dequant_word(ws.w[k16 + 1], sv, zs);
       }
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) acc[mb] = mfma32(cb, ca[mb], acc[mb]);
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(cb, ca[mb], acc[mb]);
       if (k16 + 1 < kTK / 16) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < MB; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
           __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
-  auto run = [&](auto xb, auto wb, int i) {
+  auto run = [&](auto xb, auto wb, int i) __attribute__((always_inline)) {
     constexpr int XB = decltype(xb)::value, WB = decltype(wb)::value;
     const uint16_t* xs = XB == 0 ? g_x0 : XB == 1 ? g_x1 : g_x2;
     uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;  // buffer (i + 2) % 3
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     // second launch adds the ranges in order, the LoRA term and rounds. Lane l holds four consecutive columns.
     float* pk = part + (int64_t)ks * T * w.columns;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       const int64_t p = p0 + mb * 32 + (lane & 31);
       if (p >= T) continue;
 #pragma unroll
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
   // set to zero.
   if (L.n_mats > 0 && mid != nullptr) {
-    const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kTM, T) - 1];
+    const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kRows, T) - 1];
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)(T * L.rank_cap * 2), 0x00020000);
     const int jlo = matrix_of(L, n0), jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                    0);
         }
         // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
-        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) {
+        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
           const int a = r.seg_adapter[s];
           rk = a == 0 ? 0 : min(live_rank(L, a, j) - rc, kRankChunk);
           const uint16_t* prow = L.pool + (int64_t)a * L.pool_stride;
@@ -305,14 +309,14 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             bv[k16] = *reinterpret_cast<const uint4*>(prow + boff + q);
           }
         };
-        auto apply = [&](int s, uint4 (&bv)[4], int rk) {
+        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
           if (rk <= 0) return;
           const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
 #pragma unroll
           for (int k16 = 0; k16 < 4; ++k16)
             bv[k16] = cin ? keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-          for (int mb = 0; mb < 8; ++mb) {
+          for (int mb = 0; mb < MB; ++mb) {
             const int64_t r0 = p0 + mb * 32;
             if (r0 >= se || r0 + 32 <= sb) continue;
             const int64_t row = r0 + (lane & 31);
@@ -357,6 +361,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int mb = half * 4 + mq;
+          if (mb >= MB) break;  // a 224-row tile's second half has three blocks
           const int row = mq * 32 + (lane & 31);
           const int col = (wave & 3) * 32 + g * 8 + (lane >> 5) * 4;
           const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
@@ -391,17 +396,39 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
 }  // namespace
 
+// Row-tile height for a launch: the one (256 or 224 rows) with the fewer rows per CU over all rounds of tiles, 256 on
+// a tie; split launches keep 256 (their range count is sized for 256-row tiles).
+int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
+  if (ksplit != 1) return 8;
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 8;
+  if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 0;
+  if (cus[dev] <= 0) return 8;
+  auto cost = [&](int mb) {
+    const int64_t tiles = ((tokens + 32 * mb - 1) / (32 * mb)) * n_tiles;
+    return ((tiles + cus[dev] - 1) / cus[dev]) * mb;
+  };
+  return cost(7) < cost(8) ? 7 : 8;
+}
+
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                    const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
-  const int m_tiles = (int)((r.tokens + kTM - 1) / kTM);
   const int n_tiles = (n_out + kTN - 1) / kTN;
+  const int mb = tile_blocks(r.tokens, n_tiles, ksplit);
+  const int m_tiles = (int)((r.tokens + 32 * mb - 1) / (32 * mb));
   const int64_t blocks = (int64_t)m_tiles * n_tiles * ksplit;
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);
-  hipLaunchKernelGGL(base_mfma256_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, w, L, r, x, x_stride, y,
-                     y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit);
+  if (mb == 7)
+    hipLaunchKernelGGL(base_mfma256_kernel<7>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, w, L, r, x, x_stride,
+                       y, y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit);
+  else
+    hipLaunchKernelGGL(base_mfma256_kernel<8>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, w, L, r, x, x_stride,
+                       y, y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }
