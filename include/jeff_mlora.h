@@ -5,9 +5,11 @@
  * with W = bf16((c - z) s) from packed 4-bit codes, and (A_j, sB_j) read from the pool row of token t's adapter.
  * Every entry point takes raw device pointers, sizes and a HIP stream, allocates no memory, never synchronises, and
  * returns MLORA_OK or a negative status before launching anything. No C++ exception crosses this boundary.
- * The first split product on a device creates one second stream (default priority) and two events for that device,
- * kept until the process ends: a split product's base launch runs on it beside the first factor's launch, joined
- * back to the caller's stream by event waits (which a graph capture of the caller's stream records).
+ * A split product of short segments (decode) is two launches on the caller's stream: the base ranges together with
+ * the first factor, then the epilogue. A split product forced onto long segments (MLORA_FORCE_BASE_SPLIT) creates,
+ * on its first use on a device, one second stream (default priority) and two events for that device, kept until
+ * the process ends: its base launch runs there beside the first factor's launch, joined back to the caller's stream
+ * by event waits (which a graph capture of the caller's stream records).
  *
  * Reference interfaces replaced (paths in the reference checkout, runtime/python/src/jeff_runtime/engine/):
  *   mlora_route        per-token adapter lookup adp[t // row_len]          fast_path.py:167,189; int4_kernels.py:72,113

@@ -224,8 +224,18 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* mid = static_cast<uint16_t*>(workspace);
   const bool mfma_shrink = shrink_on_mfma(route, lora->pool_rows, flags);
+  if (base == Base::split && !mfma_shrink) {
+    // split product of short segments: one launch computes the base ranges and, in further workgroups, the first
+    // factor; then the epilogue
+    const int32_t ks = split_ranges(w, route->tokens);
+    float* part = static_cast<float*>(partials);
+    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s, mid)))
+      return rc;
+    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
+  }
   if (base == Base::split) {
-    // split product: the base launch on the second stream beside the first factor's, then the epilogue
+    // split product of long segments: the base launch on the second stream beside the first factor's, then the
+    // epilogue
     const Aux* aux = aux_stream();
     if (aux == nullptr) return MLORA_ELAUNCH;
     const int32_t ks = split_ranges(w, route->tokens);
