@@ -174,17 +174,14 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
   const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * capj;
   const int64_t T = r.tokens;
   uint4 bv[CPC];
-#pragma unroll
-  for (int i = 0; i < CPC; ++i) {
-    const int col = cl + (kFinThreads / CPC) * i;
-    bv[i] = (chunk_live && col < ncols)
-                ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * capj + 8 * ch), rk - 8 * ch)
-                : make_uint4(0, 0, 0, 0);
-  }
   // the thread's four columns of one row for the base sums and the stores
   const int srow = tid / (kFinThreads / 4), scol = 4 * (tid % (kFinThreads / 4));
   for (int64_t p0 = sb; p0 < se; p0 += kRegRows) {
     const int rows = (int)min((int64_t)kRegRows, se - p0);
+    // where the thread's row goes, fetched before anything that waits
+    const int64_t prow = p0 + min(srow, rows - 1);
+    const int64_t yrow_off = (int64_t)r.tok_perm[prow] * y_stride;
+    const int q = last_out != nullptr ? r.last_of[prow] : -1;
     // base partial sums, in range order
     float4 pv[kMaxSplit];
 #pragma unroll
@@ -199,6 +196,15 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
       mv[rr] = (chunk_live && rr < rows)
                    ? keep_first(*reinterpret_cast<const uint4*>(mid + (p0 + rr) * rc + rho + 8 * ch), rk - 8 * ch)
                    : make_uint4(0, 0, 0, 0);
+    if (p0 == sb) {  // the block's sB rows, issued after the first pass's partial sums (needed first)
+#pragma unroll
+      for (int i = 0; i < CPC; ++i) {
+        const int col = cl + (kFinThreads / CPC) * i;
+        bv[i] = (chunk_live && col < ncols)
+                    ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * capj + 8 * ch), rk - 8 * ch)
+                    : make_uint4(0, 0, 0, 0);
+      }
+    }
     float4 bsum = pv[0];
 #pragma unroll
     for (int sp = 1; sp < kMaxSplit; ++sp) {
@@ -222,11 +228,9 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
     }
     __syncthreads();
     if (srow < rows && scol < ncols) {
-      const int64_t p = p0 + srow;
       const int c = oj + c0 + scol;
       const uint2 v = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
-      const int q = last_out != nullptr ? r.last_of[p] : -1;
-      uint16_t* yrow = y + (int64_t)r.tok_perm[p] * y_stride;
+      uint16_t* yrow = y + yrow_off;
       if (vec && scol + 4 <= ncols) {
         *reinterpret_cast<uint2*>(yrow + c) = v;
         if (q >= 0) *reinterpret_cast<uint2*>(last_out + (int64_t)q * n_out + c) = v;
