@@ -157,7 +157,7 @@ __device__ __forceinline__ float group_sum(float v) {
 //  - each lane dots its sB chunk with the same ranks of every row's first factor, the CPC lanes of a column add
 //    their partial sums (group_sum), and lane t % CPC == row % CPC adds the base sum and rounds into an LDS tile;
 //  - the tile's rows are written with coalesced 8-byte stores.
-template <int CPC>
+template <int CPC, int MAXS>
 __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlora_route_t& r,
                                                const float* __restrict__ part, int32_t ksplit, int32_t ld,
                                                const uint16_t* __restrict__ mid, uint16_t* __restrict__ y,
@@ -183,9 +183,9 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
     const int64_t yrow_off = (int64_t)r.tok_perm[prow] * y_stride;
     const int q = last_out != nullptr ? r.last_of[prow] : -1;
     // base partial sums, in range order
-    float4 pv[kMaxSplit];
+    float4 pv[MAXS];
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplit; ++sp)
+    for (int sp = 0; sp < MAXS; ++sp)
       pv[sp] = (sp < ksplit && srow < rows && scol < ncols)
                    ? *reinterpret_cast<const float4*>(part + ((int64_t)sp * T + p0 + srow) * ld + oj + c0 + scol)
                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -207,7 +207,7 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
     }
     float4 bsum = pv[0];
 #pragma unroll
-    for (int sp = 1; sp < kMaxSplit; ++sp) {
+    for (int sp = 1; sp < MAXS; ++sp) {
       bsum.x += pv[sp].x;
       bsum.y += pv[sp].y;
       bsum.z += pv[sp].z;
@@ -246,6 +246,8 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
 }
 
 // The register form of the split product's second launch: every matrix of the group has cap_j in {8, 16, 32, 64}.
+// MAXS: the most input ranges this form reads (1 when the base ran as one range, which frees their registers)
+template <int MAXS>
 __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlora_route_t r,
                                                             const float* __restrict__ part, int32_t ksplit,
                                                             int32_t ld, const uint16_t* __restrict__ mid,
@@ -270,19 +272,19 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlo
   const int a = r.seg_adapter[s];
   switch (L.cap[j]) {
     case 64:
-      finish_columns<8>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+      finish_columns<8, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
                         vec != 0, base_lds, out_lds);
       break;
     case 32:
-      finish_columns<4>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+      finish_columns<4, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
                         vec != 0, base_lds, out_lds);
       break;
     case 16:
-      finish_columns<2>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+      finish_columns<2, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
                         vec != 0, base_lds, out_lds);
       break;
     default:  // 8, or 0 (no adapter on this matrix: the base partial sums only)
-      finish_columns<1>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
+      finish_columns<1, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
                         vec != 0, base_lds, out_lds);
       break;
   }
@@ -307,9 +309,12 @@ int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* pa
   // 8-byte stores of four columns: 8-byte aligned output rows
   const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
                    (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0));
-  if (registers)
-    hipLaunchKernelGGL(finish_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y, y_stride,
+  if (registers && ksplit == 1)
+    hipLaunchKernelGGL(finish_kernel<1>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y, y_stride,
                        last_out, n_out, (int32_t)vec);
+  else if (registers)
+    hipLaunchKernelGGL(finish_kernel<kMaxSplit>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
+                       y_stride, last_out, n_out, (int32_t)vec);
   else
     hipLaunchKernelGGL(finish_lds_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
                        y_stride, last_out, n_out);
