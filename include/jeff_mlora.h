@@ -60,7 +60,7 @@ enum {
 /* Kernel-selection flags (0 = automatic). */
 #define MLORA_FORCE_BASE_GEMV 1
 #define MLORA_FORCE_BASE_MFMA 2
-#define MLORA_FORCE_SHRINK_GEMV 4
+#define MLORA_FORCE_SHRINK_SEGMENT 4
 #define MLORA_FORCE_SHRINK_MFMA 8
 #define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
 

@@ -64,7 +64,7 @@ bool long_segments(const mlora_route_t* r, int32_t pool_rows) {
 
 bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
   if (flags & MLORA_FORCE_SHRINK_MFMA) return true;
-  if (flags & MLORA_FORCE_SHRINK_GEMV) return false;
+  if (flags & MLORA_FORCE_SHRINK_SEGMENT) return false;
   return long_segments(r, pool_rows);
 }
 

@@ -58,7 +58,7 @@ def shrink(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, mfma: bo
     _check_input(lin, x, "shrink")
     m = x.shape[0]
     r = ws.routed(adp, lin.pool.shape[0], m)
-    flags = 0 if mfma is None else (_lib.FORCE_SHRINK_MFMA if mfma else _lib.FORCE_SHRINK_GEMV)
+    flags = 0 if mfma is None else (_lib.FORCE_SHRINK_MFMA if mfma else _lib.FORCE_SHRINK_SEGMENT)
     h = _lib.lib()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     _lib.check(h.mlora_shrink(lin.lora_abi(), r, x.data_ptr(), x.stride(0), lin.k, ws.mid.data_ptr(), flags, stream),

@@ -6,8 +6,9 @@ kernel family instead, and the tiles inside each family are fixed for gfx950.
   word), "mfma" (32x32x16 bf16 MFMA tiles, the LoRA second factor fused into the epilogue) or "split" (few tokens
   per adapter segment: MFMA tiles over ranges of the input dimension into float32 partials, then one epilogue
   workgroup per adapter segment and 256 columns).
-- shrink (the LoRA first factor): "gemv" when segments are short on average (decode: one workgroup streams 16 ranks
-  of one adapter's A) or "mfma" when they are long (prefill: 64-token tiles on MFMA).
+- shrink (the LoRA first factor): "segment" when segments are short on average (decode: one workgroup per segment
+  and 32 ranks of its adapter's A, the segment's rows as the second MFMA operand) or "mfma" when they are long
+  (prefill: 32 sorted rows per workgroup on MFMA).
 The library makes the same choice itself when no flag forces one (api.hip, shrink_on_mfma)."""
 
 from __future__ import annotations
@@ -19,7 +20,7 @@ from jeff_amd import _lib
 GEMV_MAX_TOKENS = 8
 SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT = 16
 BASES = ("gemv", "mfma", "split")
-SHRINKS = ("gemv", "mfma")
+SHRINKS = ("segment", "mfma")
 
 
 @dataclass(frozen=True)
@@ -29,7 +30,7 @@ class Int4Tiles:
 
     def flags(self) -> int:
         f = {"gemv": _lib.FORCE_BASE_GEMV, "mfma": _lib.FORCE_BASE_MFMA, "split": _lib.FORCE_BASE_SPLIT}[self.base]
-        return f | (_lib.FORCE_SHRINK_GEMV if self.shrink == "gemv" else _lib.FORCE_SHRINK_MFMA)
+        return f | (_lib.FORCE_SHRINK_SEGMENT if self.shrink == "segment" else _lib.FORCE_SHRINK_MFMA)
 
 
 def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = None,
@@ -43,4 +44,4 @@ def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = No
     segs = max(1, min(requests, pool_rows if pool_rows is not None else requests))
     long_segments = tokens >= SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT * segs
     base = "gemv" if tokens <= GEMV_MAX_TOKENS else "mfma" if long_segments else "split"
-    return Int4Tiles(base, "mfma" if long_segments else "gemv")
+    return Int4Tiles(base, "mfma" if long_segments else "segment")

@@ -44,7 +44,7 @@ def test_header_constants_match_the_binding() -> None:
     assert const("MLORA_ROUTE_BAD_ADAPTER") == _lib.ROUTE_BAD_ADAPTER
     assert const("MLORA_ROUTE_BAD_SEQLENS") == _lib.ROUTE_BAD_SEQLENS
     for name, value in (("MLORA_FORCE_BASE_GEMV", _lib.FORCE_BASE_GEMV), ("MLORA_FORCE_BASE_MFMA", _lib.FORCE_BASE_MFMA),
-                        ("MLORA_FORCE_SHRINK_GEMV", _lib.FORCE_SHRINK_GEMV),
+                        ("MLORA_FORCE_SHRINK_SEGMENT", _lib.FORCE_SHRINK_SEGMENT),
                         ("MLORA_FORCE_SHRINK_MFMA", _lib.FORCE_SHRINK_MFMA)):
         assert const(name) == value
     assert ctypes.sizeof(_lib.Int4) == 8 * 3 + 4 * 4

@@ -199,8 +199,8 @@ def reference_pattern_case(seed: int, group: int, asym: bool):
 
 @pytest.mark.parametrize("tokens,row_len", [(32, 32), (64, 64), (128, 128), (48, 16), (256, 32), (1024, 64), (4, 1),
                                             (8, 1)])
-@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "gemv"), Int4Tiles("mfma", "mfma"),
-                                   Int4Tiles("split", "gemv"), Int4Tiles("split", "mfma")])
+@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "segment"), Int4Tiles("mfma", "mfma"),
+                                   Int4Tiles("split", "segment"), Int4Tiles("split", "mfma")])
 def test_reference_pattern_products_are_within_the_bound(tokens: int, row_len: int, tiles) -> None:
     case = reference_pattern_case(tokens + row_len, 64, False)
     lin = case.lin
@@ -216,7 +216,7 @@ def test_reference_pattern_products_are_within_the_bound(tokens: int, row_len: i
 
 
 @pytest.mark.parametrize("tokens", [1, 3, 8])
-@pytest.mark.parametrize("shrink_kind", ["gemv", "mfma"])
+@pytest.mark.parametrize("shrink_kind", ["segment", "mfma"])
 def test_decode_gemv_products(tokens: int, shrink_kind: str) -> None:
     case = make_case([2048, 1024, 1024], 2048, 128, True, {a: [r, r, r] for a, r in
                                                             zip(range(1, 9), (8, 16, 32, 64, 8, 16, 32, 64))},
@@ -230,7 +230,7 @@ def test_decode_gemv_products(tokens: int, shrink_kind: str) -> None:
     assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
 
 
-@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "mfma"), Int4Tiles("mfma", "gemv"),
+@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "mfma"), Int4Tiles("mfma", "segment"),
                                    Int4Tiles("split", "mfma")])
 def test_mixed_rank_decode_batch(tiles) -> None:
     """256 one-token rows, 64 adapters of ranks 8/16/32/64, a qkv-shaped group (2048 -> 2048 + 1024 + 1024)."""
@@ -245,7 +245,7 @@ def test_mixed_rank_decode_batch(tiles) -> None:
     assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
 
 
-@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "gemv"), Int4Tiles("split", "mfma")])
+@pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "segment"), Int4Tiles("split", "mfma")])
 def test_ragged_prefill_with_last_token_gather(tiles) -> None:
     """64 requests of U{16..256} tokens, 16 adapters rank 16 on a 1024 -> 3072 g128 asymmetric group; each request's
     last-token row gathered as well."""
@@ -295,7 +295,7 @@ def test_lora_add_on_the_library_gemm_is_within_the_uncut_bound() -> None:
 def test_two_runs_and_a_graph_replay_give_the_same_bits() -> None:
     case = reference_pattern_case(21, 128, True)
     lin = case.lin
-    for tokens, row_len, tiles in ((32, 32, None), (1024, 64, None), (6, 1, None), (64, 1, Int4Tiles("mfma", "gemv")),
+    for tokens, row_len, tiles in ((32, 32, None), (1024, 64, None), (6, 1, None), (64, 1, Int4Tiles("mfma", "segment")),
                                    (64, 1, None), (1024, 64, Int4Tiles("split", "mfma"))):
         adp = torch.tensor([CYCLE[r % 4] for r in range(tokens // row_len)], dtype=torch.int32, device="cuda")
         x = torch.randn(tokens, lin.k, device="cuda").to(DT)
