@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 1
+#define MLORA_ABI_VERSION 2
 #define MLORA_MAX_MATS 8            /* matrices per fused group (the reference's largest has 4) */
 #define MLORA_MAX_REQUESTS 8192     /* request rows per routed pass */
 #define MLORA_MAX_POOL_ROWS 262144  /* adapter pool rows (row 0 = the base, no update) */
@@ -77,9 +77,16 @@ typedef struct {
 
 /* The adapter pool of one fused group. Row a of the pool (pool + a * pool_stride, bf16) holds, for this group:
  * at off_a the stacked first factors A (rank_cap, k): matrix j in rows [rho_j, rho_j + cap[j]), rho_j = sum of the
- * caps before j; at off_b[j] the second factor of matrix j, sB_j (cols[j], cap[j]), row n = output n's rank vector.
- * ranks[a * ranks_stride + j] is the live rank of matrix j in row a (0: no update); only rows [0, rank) of A_j and
- * columns [0, rank) of sB_j are read. Row 0 is the base and must have all ranks 0. */
+ * caps before j; at off_b[j] the second factor of matrix j, sB_j (cols[j], s), row n = output n's rank vector, in a
+ * block of cols[j] * cap[j] elements. The row stride s depends on the row's live rank r of matrix j:
+ * s = mlora_sb_stride(r, cap[j]) (r rounded up to a power of two, at least 8, at most cap[j]), so a low-rank adapter's
+ * sB is dense. ranks[a * ranks_stride + j] is the live rank of matrix j in row a (0: no update); only rows [0, r) of
+ * A_j and columns [0, r) of sB_j are read. Row 0 is the base and must have all ranks 0. */
+static inline int32_t mlora_sb_stride(int32_t rank, int32_t cap) {
+  int32_t s = 8;
+  while (s < rank) s <<= 1;
+  return s < cap ? s : cap;
+}
 typedef struct {
   const uint16_t* pool;
   const int32_t* ranks;

@@ -9,7 +9,7 @@ import threading
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().with_name("libjeff_mlora.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_MATS = 8
 MAX_REQUESTS = 8192
 MAX_POOL_ROWS = 262144

@@ -49,7 +49,7 @@ __device__ __forceinline__ void expand_into(f32x16_t (&acc)[2][2], int64_t prow,
           if (rank == 0) continue;
           const int oj = col_offset(L, j);
           const bool colok = c >= oj && c < oj + L.cols[j] && c < n_out;
-          const uint16_t* brow = prow_pool + L.off_b[j] + (int64_t)(colok ? c - oj : 0) * L.cap[j];
+          const uint16_t* brow = prow_pool + L.off_b[j] + (int64_t)(colok ? c - oj : 0) * sb_stride(rank, L.cap[j]);
           const uint16_t* mrow = mid + (rowok ? row : 0) * L.rank_cap + rank_offset(L, j);
           for (int k0 = 0; k0 < rank; k0 += 16) {
             const int kk = k0 + (lane >> 5) * 8;
@@ -254,7 +254,8 @@ __global__ __launch_bounds__(256) void base_gemv_kernel(mlora_int4_t w, mlora_lo
       const int j = matrix_of(L, c);
       const int rank = live_rank(L, a, j);
       const uint16_t* mr = mid + (int64_t)m * L.rank_cap + rank_offset(L, j);
-      const uint16_t* br = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)(c - col_offset(L, j)) * L.cap[j];
+      const uint16_t* br = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] +
+                             (int64_t)(c - col_offset(L, j)) * sb_stride(rank, L.cap[j]);
       for (int q = 0; q < rank; ++q) v = __builtin_fmaf(bf16_to_f32(mr[q]), bf16_to_f32(br[q]), v);
     }
     const uint16_t o = f32_to_bf16(v);

@@ -5,9 +5,9 @@
 // product (engine/int4_kernels.py:105-129), with its per-tile adapter replaced by the tile's adapter segment.
 //
 // One workgroup per (adapter segment, 256 columns of one matrix j), one column per thread. The sB rows of those
-// columns are one contiguous block of the pool row (columns x cap_j bf16), read with coalesced 16-byte loads into
-// LDS rows padded by 16 bytes (cap_j + 8 elements: the 16-byte reads of 16 consecutive rows then fall on distinct
-// banks when cap_j / 8 is even); each thread then takes its row from LDS, and the rows' first factors (the same for
+// columns are one contiguous block of the pool row (columns x the adapter's sB row stride, bf16), read with coalesced
+// 16-byte loads into LDS rows padded by 16 bytes (72 elements: the 16-byte reads of 16 consecutive rows then fall on
+// distinct banks); each thread then takes its row from LDS, and the rows' first factors (the same for
 // every thread) from LDS as well. A workgroup issues all its loads (partials, sB, first factors) before its first
 // barrier, so it waits for memory once; each adapter's sB is read once per pass, and the many small workgroups of
 // a pass keep the loads of many segments in flight.
@@ -49,11 +49,11 @@ __global__ __launch_bounds__(kFinThreads) void finish_lds_kernel(mlora_lora_t L,
   const bool cok = tid < ncols;
   const int c = oj + c0 + tid;  // output column
   const int a = r.seg_adapter[s];
-  const int capj = L.cap[j];
   const int rk = a != 0 ? live_rank(L, a, j) : 0;
+  const int sbs = sb_stride(rk, L.cap[j]);  // the adapter's sB row stride
   const int rho = rank_offset(L, j);
   const int rc = L.rank_cap;
-  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * capj;
+  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * sbs;
   const int64_t T = r.tokens;
   for (int64_t p0 = sb; p0 < se; p0 += kFinRows) {
     const int rows = (int)min((int64_t)kFinRows, se - p0);
@@ -67,13 +67,13 @@ __global__ __launch_bounds__(kFinThreads) void finish_lds_kernel(mlora_lora_t L,
         pv[sp][rr] = (cok && sp < ksplit && rr < rows) ? part[((int64_t)sp * T + p0 + rr) * ld + c] : 0.0f;
     for (int q0 = 0; q0 < max(rk, 1); q0 += kFinRanks) {
       const int nq = min(rk - q0, kFinRanks);  // live ranks of this chunk (none for the base row)
-      const int chunks = min(kFinRanks, capj - q0) / 8;
+      const int chunks = min(kFinRanks, sbs - q0) / 8;
       uint4 bv[kFinRanks / 8];
 #pragma unroll
       for (int i = 0; i < kFinRanks / 8; ++i) {
         const int e = tid + kFinThreads * i;
         const int col = e / max(chunks, 1), ch = e - col * max(chunks, 1);
-        bv[i] = (nq > 0 && col < ncols) ? *reinterpret_cast<const uint4*>(blk + (int64_t)col * capj + q0 + 8 * ch)
+        bv[i] = (nq > 0 && col < ncols) ? *reinterpret_cast<const uint4*>(blk + (int64_t)col * sbs + q0 + 8 * ch)
                                         : make_uint4(0, 0, 0, 0);
       }
       const int mrow = tid / (kFinRanks / 8), mch = tid % (kFinRanks / 8);
@@ -149,7 +149,7 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// One (segment, 256 columns of matrix j) of a matrix whose sB rows hold CPC * 8 ranks (cap_j = 8, 16, 32 or 64).
+// One (segment, 256 columns of matrix j) of an adapter whose sB rows hold CPC * 8 ranks (row stride 8, 16, 32 or 64).
 // Thread t takes 16-byte chunk t % CPC of the rows of columns t / CPC + (256 / CPC) i, i < CPC: consecutive threads
 // read consecutive 16 bytes of the contiguous sB block. Per pass of kRegRows rows:
 //  - every thread sums four columns of one row's base partials over the input ranges (coalesced 16-byte loads, all
@@ -166,12 +166,11 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
                                                bool vec, float* __restrict__ base_lds, uint16_t* __restrict__ out_lds) {
   const int tid = threadIdx.x;
   const int ch = tid % CPC, cl = tid / CPC;
-  const int capj = L.cap[j];
   const int rk = a != 0 ? live_rank(L, a, j) : 0;
   const int rho = rank_offset(L, j);
   const int rc = L.rank_cap;
   const bool chunk_live = 8 * ch < rk;
-  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * capj;
+  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)c0 * (8 * CPC);
   const int64_t T = r.tokens;
   uint4 bv[CPC];
   // the thread's four columns of one row for the base sums and the stores
@@ -201,7 +200,7 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
       for (int i = 0; i < CPC; ++i) {
         const int col = cl + (kFinThreads / CPC) * i;
         bv[i] = (chunk_live && col < ncols)
-                    ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * capj + 8 * ch), rk - 8 * ch)
+                    ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * (8 * CPC) + 8 * ch), rk - 8 * ch)
                     : make_uint4(0, 0, 0, 0);
       }
     }
@@ -245,7 +244,8 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
   }
 }
 
-// The register form of the split product's second launch: every matrix of the group has cap_j in {8, 16, 32, 64}.
+// The register form of the split product's second launch: every matrix of the group has cap_j in {0, 8, 16, 32, 64}
+// (so every adapter's sB row stride is 8, 16, 32 or 64).
 // MAXS: the most input ranges this form reads (1 when the base ran as one range, which frees their registers)
 template <int MAXS>
 __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlora_route_t r,
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlo
   const int ncols = min(kFinThreads, L.cols[j] - c0);
   if (ncols <= 0) return;
   const int a = r.seg_adapter[s];
-  switch (L.cap[j]) {
+  switch (sb_stride(a != 0 ? live_rank(L, a, j) : 0, L.cap[j])) {  // the adapter's sB row stride
     case 64:
       finish_columns<8, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
                         vec != 0, base_lds, out_lds);

@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       // the wave's column inside matrix j (others get zero operands)
       const int cc = n0 + wave * 32 + (lane & 31);
       const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
-      const int64_t boff = L.off_b[j] + (int64_t)((cin ? cc : oj) - oj) * capj;
+      const int ccol = (cin ? cc : oj) - oj;
       for (int rc = 0; rc < capj; rc += kRankChunk) {
         // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
         lds_sync();  // every wave is done with the previous chunk's rows
@@ -308,13 +308,15 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
         auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
           const int a = r.seg_adapter[s];
-          rk = a == 0 ? 0 : min(live_rank(L, a, j) - rc, kRankChunk);
-          const uint16_t* prow = L.pool + (int64_t)a * L.pool_stride;
+          const int live = a == 0 ? 0 : live_rank(L, a, j);
+          rk = min(live - rc, kRankChunk);
+          const int sbs = sb_stride(live, capj);  // the adapter's sB row stride (at least 8: capj > rc >= 0)
+          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
 #pragma unroll
           for (int k16 = 0; k16 < 4; ++k16) {
             const int kk = 16 * k16 + 8 * (lane >> 5);
-            const int q = min(rc + kk, capj - 8);
-            bv[k16] = *reinterpret_cast<const uint4*>(prow + boff + q);
+            const int q = min(rc + kk, sbs - 8);
+            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
           }
         };
         auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {

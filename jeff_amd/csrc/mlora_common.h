@@ -100,6 +100,15 @@ __device__ __forceinline__ int live_rank(const mlora_lora_t& L, int a, int j) {
   return r > L.cap[j] ? L.cap[j] : r;
 }
 
+// Row stride (elements) of sB_j in a pool row whose live rank of matrix j is `rank`: the rank rounded up to a power
+// of two, at least 8, at most cap_j (a rank-0 row keeps stride min(8, cap_j), so reads that ignore the rank stay in
+// the block). Low-rank adapters' rows are then dense: a rank-8 row is 16 bytes, not cap_j * 2.
+__device__ __forceinline__ int sb_stride(int rank, int cap) {
+  int s = 8;
+  while (s < rank) s <<= 1;
+  return s < cap ? s : cap;
+}
+
 // Stacked-rank offset rho_j and output-column offset of matrix j.
 __device__ __forceinline__ int rank_offset(const mlora_lora_t& L, int j) {
   int o = 0;

@@ -6,8 +6,11 @@ Mirrors the reference's engine/fast_path.py (paths relative to runtime/python/sr
   * each matrix j has its own rank capacity cap_j (default 16 for an adapted matrix, as the reference gives each
     one) and every adapter its own live rank r <= cap_j per matrix, held in a device table; the kernels read only
     the live ranks, so rank-8 and rank-64 adapters share a pool without padding reads;
-  * the second factor is stored per matrix as sB_j (out_j, cap_j) instead of one block-diagonal Bt (rank, out): no
+  * the second factor is stored per matrix as sB_j (out_j, s) instead of one block-diagonal Bt (rank, out): no
     zero blocks in HBM, and each output column's rank vector is one contiguous 16-byte read for the MFMA operand.
+    The row stride s is the adapter's live rank rounded up to a power of two (at least 8, at most cap_j, `sb_stride`),
+    so a low-rank adapter's sB is dense: the block reserves out_j * cap_j elements and the adapter fills the first
+    out_j * s of them.
   The first factors keep the reference layout: A (rank, k) at off_a, matrix j in rows [rho_j, rho_j + cap_j).
 - Workspace (fast_path.py:261-274): per pass shape, the scratch the products share: the LoRA first factors (mid,
   bf16, tokens x rank) and the routed pass (the sorted order of the request rows by adapter).
@@ -34,6 +37,15 @@ LORA_TARGETS = ("in_proj_qkv", "in_proj_z", "out_proj", "q_proj", "k_proj", "v_p
 DEFAULT_RANK = 16  # per adapted matrix, as the reference's fast path (fast_path.py:316)
 
 Update = tuple[torch.Tensor, torch.Tensor]  # (A (r, in), sB (out, r)): the scale alpha / r already folded into B
+
+
+def sb_stride(rank: int, cap: int) -> int:
+    """Row stride of an adapter's sB_j in the pool: its live rank rounded up to a power of two, at least 8, at most
+    cap_j (jeff_amd/csrc/mlora_common.h sb_stride; a rank-0 row keeps min(8, cap_j))."""
+    s = 8
+    while s < rank:
+        s *= 2
+    return min(s, cap)
 
 
 def fold_scale(b: torch.Tensor, scale: float, dtype: torch.dtype = DT) -> torch.Tensor:
@@ -119,7 +131,8 @@ class Lin:
                                  f"({size}, {self.k}) layer")
             a_view[self.rho[j]:self.rho[j] + r] = a
             start = self.off_bj[j] - self.off_a
-            b_view = flat[start:start + size * cap].view(size, cap)
+            stride = sb_stride(r, cap)
+            b_view = flat[start:start + size * stride].view(size, stride)
             b_view[:, :r] = sb
             live.append(r)
         return live

@@ -11,8 +11,9 @@ from oracle import codec
 
 def adapters_of(lin, rows) -> dict:
     """{pool row: [(A (r, k), sB (out_j, r)) or None per matrix]} of a bound jeff_amd Lin, read from the device.
-    The layout read here is the pool's: A (rank, k) at off_a with matrix j in rows rho_j.., then sB_j (out_j, cap_j)
-    at off_bj[j]; only the live ranks (the ranks table) are returned."""
+    The layout read here is the pool's: A (rank, k) at off_a with matrix j in rows rho_j.., then sB_j at off_bj[j],
+    (out_j, s) with row stride s = the live rank r rounded up to a power of two, at least 8, at most cap_j; only the
+    live ranks (the ranks table) are returned."""
     out = {}
     n = len(lin.names)
     for row in rows:
@@ -28,7 +29,8 @@ def adapters_of(lin, rows) -> dict:
                 ups.append(None)
                 continue
             start = lin.off_bj[j] - lin.off_a
-            sb = flat[start:start + size * cap].view(size, cap)[:, :r].contiguous()
+            stride = min(max(8, 1 << (r - 1).bit_length()), cap)
+            sb = flat[start:start + size * stride].view(size, stride)[:, :r].contiguous()
             ups.append((a_all[lin.rho[j]:lin.rho[j] + r].contiguous(), sb))
         out[row] = ups
     return out

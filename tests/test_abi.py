@@ -14,7 +14,8 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "jeff_mlora.h"
 
 
 def declared() -> set[str]:
-    return set(re.findall(r"^\w[\w\s\*]*?\b(mlora_\w+)\(", HEADER.read_text(), flags=re.M))
+    """The entry points the header declares (its static inline helpers are not exported)."""
+    return set(re.findall(r"^(?!static)\w[\w\s\*]*?\b(mlora_\w+)\(", HEADER.read_text(), flags=re.M))
 
 
 def test_every_declared_entry_point_is_exported() -> None:
@@ -66,3 +67,19 @@ def test_workspace_bytes_and_refusals_before_any_launch() -> None:
     assert h.mlora_route(16, None, 1, ctypes.byref(r), 4, None) == _lib.EINVAL  # max_segs < min(requests, rows)
     assert h.mlora_route(16, None, 2, ctypes.byref(_lib.Route(16, 16, 16, 16, 16, 16, 16, 16, 10, 10, 4)), 4,
                          None) == _lib.EINVAL  # 10 rows of 2 tokens are not 10 tokens
+
+
+def test_header_stride_helper_matches_the_package(tmp_path: Path) -> None:
+    """mlora_sb_stride (the header's rule for an adapter's sB row stride) gives what Lin.pack uses."""
+    from jeff_amd.fast_path import sb_stride
+
+    src = tmp_path / "s.c"
+    src.write_text('#include "jeff_mlora.h"\n#include <stdio.h>\nint main(void) {\n'
+                   '  for (int c = 0; c <= 128; c += 8)\n    for (int r = 0; r <= c; ++r)\n'
+                   '      printf("%d %d %d\\n", r, c, mlora_sb_stride(r, c));\n  return 0;\n}\n')
+    exe = tmp_path / "s"
+    subprocess.run(["gcc", "-std=c99", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    rows = [tuple(map(int, line.split())) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                      check=True).stdout.splitlines()]
+    assert len(rows) == sum(c + 1 for c in range(0, 129, 8))
+    assert all(s == sb_stride(r, c) for r, c, s in rows)

@@ -7,12 +7,13 @@ from __future__ import annotations
 import pytest
 import torch
 
-from jeff_amd.fast_path import DT, AdapterPool, Lin, Workspace, fold_scale
+from jeff_amd.fast_path import DT, AdapterPool, Lin, Workspace, fold_scale, sb_stride
 from jeff_amd.int4 import Int4Error, pack_kernel, pack_kernel_asym, unpack_kernel, unpack_kernel_asym
 from jeff_amd.int4_kernels import int4_product
 from jeff_amd.int4_tiles import Int4Tiles, int4_tiles
 from jeff_amd.product_choice import (CUBLAS, INT4, PAIRS, PRODUCTS, ProductChoice, choose_product,
                                      product_candidates)
+from oracle import pool_view
 
 
 def test_pack_writes_a_rows_and_per_matrix_second_factors() -> None:
@@ -26,11 +27,40 @@ def test_pack_writes_a_rows_and_per_matrix_second_factors() -> None:
     flat = pool.lora_pool[1]
     a = flat[:24 * 32].view(24, 32)
     assert torch.equal(a[0:8], a0) and bool((a[8:16] == 0).all()) and torch.equal(a[16:24], a1)
-    bq = flat[lin.off_bj[0]:lin.off_bj[0] + 24 * 16].view(24, 16)
+    # sB rows at the live rank's stride (rank 8 in a rank-16 block: 8 elements per row, the rest of the block zero)
+    bq = flat[lin.off_bj[0]:lin.off_bj[0] + 24 * 8].view(24, 8)
+    assert torch.equal(bq, b0) and bool((flat[lin.off_bj[0] + 24 * 8:lin.off_bj[1]] == 0).all())
     bk = flat[lin.off_bj[1]:lin.off_bj[1] + 16 * 8].view(16, 8)
-    assert torch.equal(bq[:, :8], b0) and bool((bq[:, 8:] == 0).all()) and torch.equal(bk, b1)
+    assert torch.equal(bk, b1)
     with pytest.raises(ValueError, match="does not fit the fast path's rank-8 buffer"):
         pool.add_adapter("big", {"l.k_proj": (torch.zeros(16, 32, dtype=DT), torch.zeros(16, 16, dtype=DT))})
+
+
+def test_second_factor_stride_follows_the_live_rank() -> None:
+    """sB rows are stored at the live rank rounded up to a power of two (at least 8, at most the capacity), and the
+    oracle's pool reader applies the same rule: adapters of every rank read back exactly what was packed."""
+    assert [sb_stride(r, 64) for r in (0, 1, 8, 9, 16, 17, 33, 64)] == [8, 8, 8, 16, 16, 32, 64, 64]
+    assert [sb_stride(r, 48) for r in (0, 33, 48)] == [8, 48, 48] and sb_stride(0, 0) == 0
+    lin = Lin(["l.q_proj", "l.k_proj"], sizes=[40, 24], k=16, ranks=[64, 48])
+    pool = AdapterPool([lin], 8, device="cpu")
+    g = torch.Generator().manual_seed(3)
+
+    def update(r: int, n: int):
+        return torch.randn(r, 16, generator=g).to(DT), torch.randn(n, r, generator=g).to(DT)
+
+    packed = {}
+    for i, (rq, rk) in enumerate([(1, 33), (8, 48), (9, 1), (17, 24), (33, 0), (64, 47)]):
+        ups = {"l.q_proj": update(rq, 40)}
+        if rk:
+            ups["l.k_proj"] = update(rk, 24)
+        packed[pool.add_adapter(f"a{i}", ups)] = ups
+    got = pool_view.adapters_of(lin, packed)
+    for row, ups in packed.items():
+        for j, name in enumerate(lin.names):
+            if name not in ups:
+                assert got[row][j] is None
+                continue
+            assert torch.equal(got[row][j][0], ups[name][0]) and torch.equal(got[row][j][1], ups[name][1])
 
 
 def test_pool_rows_lowest_free_first_base_row_zero_and_refusals() -> None:
