@@ -5,8 +5,10 @@
  * with W = bf16((c - z) s) from packed 4-bit codes, and (A_j, sB_j) read from the pool row of token t's adapter.
  * Every entry point takes raw device pointers, sizes and a HIP stream, allocates no memory, never synchronises, and
  * returns MLORA_OK or a negative status before launching anything. No C++ exception crosses this boundary.
- * A split product of short segments (decode) is two launches on the caller's stream: the base ranges together with
- * the first factor, then the epilogue. A split product forced onto long segments (MLORA_FORCE_BASE_SPLIT) creates,
+ * A narrow product (at most 256 tokens, few per adapter segment: decode) is two launches on the caller's stream, the
+ * first factor then the base product with the second factor fused, plus a third that adds the float32 ranges when
+ * the input dimension is split. A split product of short segments (more tokens) is two launches: the base ranges
+ * together with the first factor, then the epilogue. A split product forced onto long segments (MLORA_FORCE_BASE_SPLIT) creates,
  * on its first use on a device, one second stream (default priority) and two events for that device, kept until
  * the process ends: its base launch runs there beside the first factor's launch, joined back to the caller's stream
  * by event waits (which a graph capture of the caller's stream records).
@@ -63,6 +65,8 @@ enum {
 #define MLORA_FORCE_SHRINK_SEGMENT 4
 #define MLORA_FORCE_SHRINK_MFMA 8
 #define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
+#define MLORA_FORCE_BASE_NARROW 32  /* narrow product (at most 256 tokens): every token in one row tile of 64 columns */
+#define MLORA_FORCE_RANGES(s) ((s) << 8)  /* a narrow product over s = 1, 2, 4 or 8 input ranges (s dividing k / 64) */
 
 /* INT4 weights in the kernel layout (reference int4.py:215-230, plus zero points and g128):
  * words  int32 (k/8, columns): word i of column c holds inputs 8i..8i+7, input 8i+j in bits 4j..4j+3 (the code c);
@@ -141,8 +145,9 @@ int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uin
 
 /* Bytes of float32 partial products the product of `w` over `route` needs with these flags; 0 when it runs the
  * fused kernels. Passes with few tokens per adapter segment (decode) split the input dimension into ranges whose
- * float32 sums a second launch adds in order (the reference's split product); its size depends on the token count,
- * the group's columns and inputs, not on device memory, so a caller can size its buffer once per shape. */
+ * float32 sums a later launch adds in order (the reference's split product); its size depends on the token count,
+ * the group's columns and inputs and the device's CU count, not on device memory, so a caller can size its buffer
+ * once per shape. */
 size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                                  int32_t flags);
 

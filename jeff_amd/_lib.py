@@ -28,6 +28,13 @@ ERRORS = {EINVAL: "invalid argument (a null pointer, a bad size or shape)",
 ROUTE_BAD_ADAPTER = 1
 ROUTE_BAD_SEQLENS = 2
 FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_SEGMENT, FORCE_SHRINK_MFMA, FORCE_BASE_SPLIT = 1, 2, 4, 8, 16
+FORCE_BASE_NARROW = 32
+
+
+def force_ranges(s: int) -> int:
+    """MLORA_FORCE_RANGES(s): a narrow product over s input ranges."""
+    return s << 8
+
 
 EXPORTS = ("mlora_abi_version", "mlora_workspace_bytes", "mlora_int4_partials_bytes", "mlora_route", "mlora_dequant",
            "mlora_shrink", "mlora_int4_linear", "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits",

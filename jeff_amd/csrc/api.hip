@@ -68,7 +68,9 @@ bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
   return long_segments(r, pool_rows);
 }
 
-enum class Base { gemv, fused, split };
+enum class Base { gemv, fused, split, narrow };
+
+constexpr int64_t kNarrowMaxTokens = 256;  // the narrow kernel's row tile holds every token of the pass
 
 // The split product runs the 256 x 256 kernel (32-bit x offsets) and stages first factors of at most
 // MLORA_SPLIT_MAX_RANK stacked ranks.
@@ -76,23 +78,63 @@ bool split_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_
   return L->rank_cap <= MLORA_SPLIT_MAX_RANK && r->tokens * (x_stride > w->k ? x_stride : w->k) < ((int64_t)1 << 31);
 }
 
-// Which base kernels run; EUNSUPPORTED when the flags force one that cannot.
+// Which base kernels run; EUNSUPPORTED when the flags force one that cannot (forced input ranges: a count of 1, 2,
+// 4 or 8 dividing the 64-input steps, for a narrow product only).
 int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
             Base* out) {
+  const int32_t fs = (flags >> 8) & 0xF;
+  if (fs != 0 && (!(fs == 1 || fs == 2 || fs == 4 || fs == 8) || (w->k / 64) % fs)) return MLORA_EUNSUPPORTED;
   if (flags & MLORA_FORCE_BASE_GEMV) {
     if (r->tokens > 8) return MLORA_EUNSUPPORTED;
     *out = Base::gemv;
   } else if (flags & MLORA_FORCE_BASE_SPLIT) {
     if (!split_fits(w, L, r, x_stride)) return MLORA_EUNSUPPORTED;
     *out = Base::split;
+  } else if (flags & MLORA_FORCE_BASE_NARROW) {
+    if (r->tokens > kNarrowMaxTokens || !split_fits(w, L, r, x_stride)) return MLORA_EUNSUPPORTED;
+    *out = Base::narrow;
   } else if (flags & MLORA_FORCE_BASE_MFMA) {
     *out = Base::fused;
   } else if (r->tokens <= 8) {
     *out = Base::gemv;
+  } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
+    *out = Base::fused;
   } else {
-    *out = !long_segments(r, L->pool_rows) && split_fits(w, L, r, x_stride) ? Base::split : Base::fused;
+    *out = r->tokens <= kNarrowMaxTokens ? Base::narrow : Base::split;
   }
-  return MLORA_OK;
+  return fs != 0 && *out != Base::narrow ? MLORA_EUNSUPPORTED : MLORA_OK;
+}
+
+// CUs of the current device (256 when it cannot be asked, e.g. on a host without a GPU).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0 && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                        cus[dev] <= 0))
+    cus[dev] = 256;
+  return cus[dev];
+}
+
+// Input ranges of a narrow product: the forced count, else the count S in {1, 2, 4, 8} (dividing the 64-input steps)
+// with the least estimated time. A workgroup takes about 0.45 us per step plus 4 us of fixed work, in rounds of one per CU; a split
+// adds a launch (4 us) and the float32 ranges' round trip through memory at 5 TB/s.
+int32_t narrow_ranges(const mlora_int4_t* w, int32_t flags) {
+  if ((flags >> 8) & 0xF) return (flags >> 8) & 0xF;  // forced (base_of checked it)
+  const int64_t tiles = w->columns / 64, steps = w->k / 64, cus = device_cus();
+  double best = 0.0;
+  int32_t pick = 1;
+  for (int32_t s = 1; s <= 8; s *= 2) {
+    if (steps % s) continue;
+    const int64_t rounds = (tiles * s + cus - 1) / cus;
+    double t = (double)rounds * (0.45 * (double)(steps / s) + 4.0);
+    if (s > 1) t += 4.0 + (double)dec_partials_bytes(*w, s) * 2.0 / 5.0e6;
+    if (s == 1 || t < best) {
+      best = t;
+      pick = s;
+    }
+  }
+  return pick;
 }
 
 // Input ranges of a split product: the most (at most 8, each of at least 4 steps of 64 inputs, dividing the steps)
@@ -137,7 +179,14 @@ const Aux* aux_stream() {
 // The base product (and the LoRA second factor) once mid holds the first factors.
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
-             void* partials, size_t partials_bytes, Base base, hipStream_t s) {
+             void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
+  if (base == Base::narrow) {
+    const int32_t ks = narrow_ranges(w, flags);
+    const size_t need = dec_partials_bytes(*w, ks);
+    if (need > 0 && (partials == nullptr || !aligned16(partials) || partials_bytes < need)) return MLORA_EWORKSPACE;
+    return launch_dec(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, static_cast<float*>(partials), ks,
+                      s);
+  }
   if (base != Base::split)
     return launch_base(w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, base == Base::gemv, s);
   if (partials == nullptr || !aligned16(partials) || partials_bytes < split_bytes(w, r->tokens))
@@ -201,8 +250,9 @@ size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora
                                  int32_t flags) {
   if (check_int4(w) || check_route(route) || check_lora(lora, w->k, w->out) || route->tokens == 0) return 0;
   Base base;
-  if (base_of(w, lora, route, w->k, flags, &base) || base != Base::split) return 0;
-  return split_bytes(w, route->tokens);
+  if (base_of(w, lora, route, w->k, flags, &base)) return 0;
+  if (base == Base::narrow) return dec_partials_bytes(*w, narrow_ranges(w, flags));
+  return base == Base::split ? split_bytes(w, route->tokens) : 0;
 }
 
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
@@ -251,7 +301,8 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
   }
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
-  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, s);
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
+                  s);
 }
 
 int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
@@ -265,7 +316,7 @@ int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, cons
   if (y == nullptr || y_stride < w->out || mid == nullptr || !aligned16(mid)) return MLORA_EINVAL;
   Base base;
   if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
-  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base,
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
                   static_cast<hipStream_t>(stream));
 }
 

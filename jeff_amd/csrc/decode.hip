@@ -1,0 +1,446 @@
+// Decode-sized INT4 product (every token of the pass in one row tile, at most 256, few tokens per adapter segment):
+//   y[perm[p], c] = bf16( sum_k x[perm[p], k] W[c, k] + sum_q mid[p, rho_j + q] sB_j[a(p)][c - o_j, q] )
+// The same arithmetic as the prefill kernel (gemm256.hip), tiled for few rows: a tile is all of the pass's sorted
+// rows x 64 columns, so a product spreads over the CUs with few or no splits of the input dimension (a 12288-column
+// product runs as 192 workgroups over all 2048 inputs). 8 waves in 4 row groups x 2 column groups: a wave owns 64
+// rows x 32 columns (two 32x32 MFMA blocks). A step's packed words are loaded and dequantised once for the
+// workgroup (one word per thread) into an LDS buffer that every wave reads its weight operands from, and each wave
+// reads its 64 rows of x from an LDS ring that buffer loads with the LDS flag fill, as in the prefill kernel; words
+// and x rows are loaded three steps ahead.
+// When the columns alone are too few for the CUs, the input dimension is split into S ranges: each range writes its
+// float32 tile in the accumulators' own order (one coalesced 1 KB store per MFMA block and column group), and
+// dec_reduce_kernel adds the ranges in order and rounds once.
+// LoRA: the first factors of the wave's rows (64 ranks of matrix j) are loaded once; the adapter segments crossing
+// those rows are listed one per lane (adapter, live rank), and their sB operands stream from memory four segments
+// ahead of the MFMAs (with S input ranges, range ks takes every S-th of the wave's segments from the ks-th). A segment's term goes into the row blocks it crosses, with the first
+// factors of rows outside the segment, and ranks past its live rank, set to zero.
+#include <type_traits>
+
+#include "tile_common.h"
+
+namespace {
+
+using namespace mlora;
+
+constexpr int kDThreads = 512;
+constexpr int kDRows = 256;               // rows of the tile: every token of the pass
+constexpr int kDCG = 2;                   // column groups of 32 (tile of 64 columns)
+constexpr int kDRG = 8 / kDCG;            // row groups
+constexpr int kDMB = kDRows / kDRG / 32;  // 32-row MFMA blocks per wave
+constexpr int kDCols = 32 * kDCG;
+constexpr int kDXLoads = 4;               // x rows: LDS-flag buffer loads per lane and step
+constexpr int kDWLoads = 3;               // weights: a word, a scale and a zero point per thread and step
+constexpr int kDRankChunk = 64;           // ranks of a matrix per LoRA pass
+constexpr int kDRedThreads = 256;
+
+static_assert(kDRows / kDRG == 32 * kDMB, "row groups must cover the tile");
+
+__shared__ __attribute__((aligned(16))) uint16_t d_x0[kDRows * kTK];
+__shared__ __attribute__((aligned(16))) uint16_t d_x1[kDRows * kTK];
+__shared__ __attribute__((aligned(16))) uint16_t d_x2[kDRows * kTK];
+__shared__ __attribute__((aligned(16))) uint16_t d_x3[kDRows * kTK];
+__shared__ uint4 d_w0[8 * kDCols];  // a step's weights, dequantised: 8 input octets x 64 columns of 8 bf16
+__shared__ uint4 d_w1[8 * kDCols];
+__shared__ int32_t d_orig[kDRows];  // the tile's rows: original token index, -1 past the tokens
+__shared__ int32_t d_last[kDRows];  // the tile's rows: request whose last token it is, else -1
+
+// Float4 index of (range ks, column tile nt, wave, block mb, column group g, lane) in the split partial tiles.
+__device__ __forceinline__ int64_t part_index(int ks, int n_tiles, int nt, int wave, int mb, int g, int lane) {
+  return ((((int64_t)ks * n_tiles + nt) * 8 + wave) * kDMB * 4 + mb * 4 + g) * 64 + lane;
+}
+
+__global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
+                                                        const uint16_t* __restrict__ x, int64_t x_stride,
+                                                        uint16_t* __restrict__ y, int64_t y_stride,
+                                                        uint16_t* __restrict__ last_out, int32_t n_out,
+                                                        const uint16_t* __restrict__ mid, int32_t n_tiles,
+                                                        int32_t vec, float4* __restrict__ part, int32_t ksplit) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
+  const int cg = wave % kDCG, rg = wave / kDCG;
+  // block -> (input range ks, column tile nt), column tiles innermost: blocks of one range (the same x) share an XCD
+  const int blocks = n_tiles * ksplit;
+  const int b = xcd_tile(blockIdx.x, blocks);
+  const int ks = b / n_tiles, nt = b - ks * n_tiles;
+  const int T = (int)r.tokens;
+  const int n0 = nt * kDCols;
+  const int R0 = rg * 32 * kDMB;  // the wave's first row
+
+  const __amdgpu_buffer_rsrc_t xres =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)0xFFFFFFFFu, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)w.words, (short)0, (int)((int64_t)(w.k / 8) * w.columns * 4), 0x00020000);
+  const int64_t groups = w.k / w.group;
+  const int gshift = w.group == 128 ? 7 : 6;  // the host accepts groups of 64 and 128 inputs
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)w.scales, (short)0, (int)(groups * w.columns * 2), 0x00020000);
+  const bool asym = w.zeros != nullptr;
+  const __amdgpu_buffer_rsrc_t zres = __builtin_amdgcn_make_buffer_rsrc(
+      asym ? (void*)w.zeros : (void*)w.scales, (short)0, (int)(groups * w.columns), 0x00020000);
+
+  if (tid < kDRows) {
+    const bool mine = tid < T;
+    d_orig[tid] = mine ? r.tok_perm[tid] : -1;
+    d_last[tid] = (mine && last_out != nullptr) ? r.last_of[tid] : -1;
+  }
+  // x: instruction i of wave `wave` fills rows (8 i + wave) * 8 .. +7; lane l writes LDS chunk slot l & 7 of row
+  // +(l >> 3), which holds logical chunk (l & 7) ^ (l >> 3). Rows past the tokens read row 0 of the pass.
+  uint32_t xoff[kDXLoads];
+#pragma unroll
+  for (int i = 0; i < kDXLoads; ++i) {
+    const int row = (8 * i + wave) * 8 + (lane >> 3);
+    xoff[i] = (uint32_t)(((int64_t)r.tok_perm[row < T ? row : 0] * x_stride + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+  }
+  auto dma_x = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kDXLoads; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(buf + (8 * i + wave) * 8 * kTK), 16, xoff[i], kc * 2,
+                                               0, 0);
+  };
+
+  // weights: thread t loads word t / 64 of the step (inputs 8 (t / 64) .. +7) of column n0 + t % 64 with that
+  // column's raw scale and zero point, and dequantises it once for the whole workgroup into the step's LDS buffer, at
+  // 16-byte chunk t, where the MFMA operand of (column, inputs) reads it; columns past the layout read column 0 and
+  // get zero weights (scale 0)
+  const int wcol = n0 + (tid & (kDCols - 1));
+  const bool colok = wcol < w.columns;
+  const uint32_t gcol = colok ? wcol : 0;
+  const uint32_t woff = (gcol + (uint32_t)(tid / kDCols) * w.columns) * 4;
+  const uint32_t soff = gcol * 2;
+  const uint32_t zoff = asym ? gcol : gcol * 2;
+  auto fetch_w = [&](WStage& st, int kc) __attribute__((always_inline)) {
+    st.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wres, woff, (kc / 8) * w.columns * 4, 0);
+    const int g = (kc >> gshift) * w.columns;
+    st.sbits = __builtin_amdgcn_raw_buffer_load_b16(sres, soff, g * 2, 0);
+    st.zbyte = __builtin_amdgcn_raw_buffer_load_b8(zres, zoff, asym ? g : g * 2, 0);
+  };
+  auto dequant_to = [&](uint4* wb, const WStage& st) __attribute__((always_inline)) {
+    const float s0v = bf16_to_f32(st.sbits);
+    const float zv = asym ? (float)st.zbyte : 8.0f;
+    wb[tid] = dequant_word(st.w[0], colok ? s0v : 0.0f, colok ? zv * s0v : 0.0f);
+  };
+
+  f32x16_t acc[kDMB];
+#pragma unroll
+  for (int mb = 0; mb < kDMB; ++mb) acc[mb] = f32x16_t{};
+
+  // first factors of the wave's rows R0 + 32 mb + (lane & 31), ranks rc + 16 k16 + 8 (lane >> 5) .. +7 of matrix j
+  // (zero past the pass's rows and past cap_j)
+  auto load_mid = [&](uint4 (&m)[kDMB][4], int j, int rc) __attribute__((always_inline)) {
+    const int capj = L.cap[j], rho = rank_offset(L, j);
+    const int rows = min(R0 + 32 * kDMB, T);
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+      for (int k16 = 0; k16 < 4; ++k16) {
+        const int row = R0 + mb * 32 + (lane & 31);
+        const int q = rc + 16 * k16 + 8 * (lane >> 5);
+        m[mb][k16] = (row < rows && q < capj)
+                         ? *reinterpret_cast<const uint4*>(mid + (int64_t)row * L.rank_cap + rho + q)
+                         : make_uint4(0, 0, 0, 0);
+      }
+  };
+
+  // the wave's rows R0 + 32 mb + (lane & 31), read as one index into the LDS array (keeps the array known)
+  auto load_a = [&](const uint16_t* xs, int k16, uint4 (&a)[kDMB]) __attribute__((always_inline)) {
+    const int c = 2 * k16 + (lane >> 5);
+    const uint4* xv = reinterpret_cast<const uint4*>(xs);
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) a[mb] = xv[swz(R0 + mb * 32 + (lane & 31), c) >> 3];
+  };
+  // the wave's weight operand for 16 inputs k16: chunk (2 k16 + (lane >> 5)) * 64 + 32 cg + (lane & 31)
+  auto load_w = [&](const uint4* wb, int k16) __attribute__((always_inline)) {
+    return wb[(2 * k16 + (lane >> 5)) * kDCols + cg * 32 + (lane & 31)];
+  };
+  // A step's operands, all read from LDS before its MFMAs (8 MFMAs per wave are too few to hide a read's latency one
+  // 16-input slice at a time).
+  auto read_ops = [&](const uint16_t* xs, const uint4* wb, uint4 (&a)[kTK / 16][kDMB], uint4 (&b)[kTK / 16])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int k16 = 0; k16 < kTK / 16; ++k16) {
+      load_a(xs, k16, a[k16]);
+      b[k16] = load_w(wb, k16);
+    }
+  };
+  auto mfma_k16 = [&](const uint4 (&a)[kDMB], const uint4& b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) acc[mb] = mfma32(b, a[mb], acc[mb]);
+  };
+
+  // LoRA bookkeeping issued before the K loop so its loads land during it: each lane's row of block mb and
+  // that row's segment (-1 past the pass), and the first factors of the wave's rows for the first matrix of its
+  // columns (ranks 0..63); the segments' adapters and live ranks follow once the segment range is known.
+  const int cw0 = n0 + cg * 32;  // the wave's first column
+  const int r_end = min(R0 + 32 * kDMB, T);
+  const bool lora = L.n_mats > 0 && mid != nullptr && cw0 < n_out && R0 < r_end;
+  const int jlo = lora ? matrix_of(L, cw0) : 0;
+  int rseg[kDMB];
+  uint4 m0[kDMB][4];
+  if (lora) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) {
+      const int row = R0 + mb * 32 + (lane & 31);
+      rseg[mb] = row < r_end ? r.seg_of[row] : -1;
+    }
+    load_mid(m0, jlo, 0);
+  }
+
+  // Step i reads x buffer i % 4 (its rows loaded at the start of step i - 3) and dequantised weight buffer i % 2
+  // (written during step i - 1 from the words loaded at the start of step i - 3): a step of this narrow tile is short
+  // (8 MFMAs per wave), so the loads run three steps ahead. Every load is unconditional (past the last step it
+  // re-reads the last one), so the number of loads in flight at each wait is the same on every path; a step's words
+  // are issued before its x rows (loads complete in order).
+  const int nk = w.k / kTK / ksplit;  // this block's K steps, from step ks * nk
+  const int kbase = ks * nk * kTK;
+  WStage s0, s1, s2, s3;
+  fetch_w(s0, kbase);
+  dma_x(d_x0, kbase);
+  fetch_w(s1, kbase + min(1, nk - 1) * kTK);
+  dma_x(d_x1, kbase + min(1, nk - 1) * kTK);
+  fetch_w(s2, kbase + min(2, nk - 1) * kTK);
+  dma_x(d_x2, kbase + min(2, nk - 1) * kTK);
+  // per block, the segments it crosses; the wave's segments (at most 64: one per row), one per lane: its adapter
+  int blo[kDMB], bhi[kDMB], s_lo = 0, s_hi = -1, la = 0, llive0 = 0;
+  if (lora) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) {
+      const int last = r_end - 1 - (R0 + mb * 32);  // the block's last row in the pass, relative to its first
+      blo[mb] = last >= 0 ? __builtin_amdgcn_readfirstlane(rseg[mb]) : INT_MAX;
+      bhi[mb] = last >= 0 ? __builtin_amdgcn_readlane(rseg[mb], min(last, 31)) : -1;
+    }
+    s_lo = blo[0];
+    s_hi = bhi[kDMB - 1] >= 0 ? bhi[kDMB - 1] : bhi[0];
+    la = s_lo + lane <= s_hi ? r.seg_adapter[s_lo + lane] : 0;
+  }
+  // landed: step 0's words and x rows and step 1's words (step 1's x rows and step 2's loads may be in flight)
+  MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
+  dequant_to(d_w0, s0);
+  step_sync();
+  auto run = [&](auto slot, int i) __attribute__((always_inline)) {
+    constexpr int B = decltype(slot)::value;
+    const uint16_t* xs = B == 0 ? d_x0 : B == 1 ? d_x1 : B == 2 ? d_x2 : d_x3;
+    uint16_t* xf = B == 0 ? d_x3 : B == 1 ? d_x0 : B == 2 ? d_x1 : d_x2;  // buffer (i + 3) % 4
+    WStage& wn = B == 0 ? s1 : B == 1 ? s2 : B == 2 ? s3 : s0;            // step i + 1's words
+    WStage& wf = B == 0 ? s3 : B == 1 ? s0 : B == 2 ? s1 : s2;            // step i + 3's words (fetched now)
+    // The step's MFMAs go in between the loads for step i + 3 (words before x rows: loads complete in order) and
+    // the dequantisation of step i + 1's words into the weight buffer step i - 1 read, so the matrix core works
+    // while the wave issues them; the scheduling barriers keep that order.
+    uint4 a[kTK / 16][kDMB], b[kTK / 16];
+    read_ops(xs, (B & 1) ? d_w1 : d_w0, a, b);
+    mfma_k16(a[0], b[0]);
+    fetch_w(wf, kbase + min(i + 3, nk - 1) * kTK);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_k16(a[1], b[1]);
+    dma_x(xf, kbase + min(i + 3, nk - 1) * kTK);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_k16(a[2], b[2]);
+    dequant_to((B & 1) ? d_w0 : d_w1, wn);
+    mfma_k16(a[3], b[3]);
+    // landed: step i + 1's x rows and step i + 2's words (step i + 2's x rows and step i + 3's loads in flight)
+    MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
+    step_sync();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  for (int it = 0; it < nk; it += 4) {
+    run(I0{}, it);
+    if (it == 0 && lora) llive0 = la == 0 ? 0 : live_rank(L, la, jlo);  // lands during the next steps
+    if (it + 1 >= nk) break;
+    run(I1{}, it + 1);
+    if (it + 2 >= nk) break;
+    run(I2{}, it + 2);
+    if (it + 3 >= nk) break;
+    run(I3{}, it + 3);
+  }
+  MLORA_WAIT_VM(0);
+
+  // LoRA second factor: this range's share of the segments s_lo..s_hi crossing the wave's rows
+  if (lora) {
+    const int cc = cw0 + (lane & 31);
+    const int jhi = matrix_of(L, min(cw0 + 31, n_out - 1));
+    for (int j = jlo; j <= jhi; ++j) {
+      const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j];
+      const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
+      const bool allin = cw0 >= oj && cw0 + 32 <= oj + cj && cw0 + 32 <= n_out;  // every lane's column in matrix j
+      const int ccol = (cin ? cc : oj) - oj;
+      const int llive = j == jlo ? llive0 : (la == 0 ? 0 : live_rank(L, la, j));
+      for (int rc = 0; rc < capj; rc += kDRankChunk) {
+        uint4 m[kDMB][4];
+        if (j == jlo && rc == 0) {
+#pragma unroll
+          for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) m[mb][k16] = m0[mb][k16];
+        } else {
+          load_mid(m, j, rc);
+        }
+        // sB operands of segment s (ranks rc + 16 k16 + 8 (lane >> 5) .. +7): unconditional loads inside the
+        // adapter's block (clamped to its last 8 ranks), masked when used
+        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+          const int i = min(s, s_hi) - s_lo;
+          const int a = __builtin_amdgcn_readlane(la, i);
+          const int live = __builtin_amdgcn_readlane(llive, i);
+          rk = s <= s_hi ? min(live - rc, kDRankChunk) : 0;
+          const int sbs = sb_stride(live, capj);  // at least 8: capj > rc >= 0
+          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
+            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+          }
+        };
+        // Chunks wholly inside the live rank go in unmasked; the one chunk crossing it (rk not a multiple of 16)
+        // keeps its live ranks in both operands. Rows outside the segment get zero first factors.
+        auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+          if (rk <= 0) return;
+          bool mine[kDMB];
+#pragma unroll
+          for (int mb = 0; mb < kDMB; ++mb) mine[mb] = rseg[mb] == s;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            if (16 * k16 >= rk) break;
+            const bool edge = 16 * k16 + 16 > rk;
+            const int n = rk - (16 * k16 + 8 * (lane >> 5));
+            uint4 bm = edge ? keep_first(bv[k16], n) : bv[k16];
+            if (!allin) bm = cin ? bm : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < kDMB; ++mb) {
+              if (s < blo[mb] || s > bhi[mb]) continue;
+              uint4 am = mine[mb] ? m[mb][k16] : make_uint4(0, 0, 0, 0);
+              if (edge) am = keep_first(am, n);
+              acc[mb] = mfma32(bm, am, acc[mb]);
+            }
+          }
+        };
+        uint4 q0[4], q1[4], q2[4], q3[4];
+        int k0, k1, k2, k3;
+        // input range ks takes segments s_lo + ks, s_lo + ks + S, ... (the ranges' sums are added afterwards)
+        const int S = ksplit;
+        load_b(s_lo + ks, q0, k0);
+        load_b(s_lo + ks + S, q1, k1);
+        load_b(s_lo + ks + 2 * S, q2, k2);
+        load_b(s_lo + ks + 3 * S, q3, k3);
+        for (int s = s_lo + ks; s <= s_hi; s += 4 * S) {
+          apply(s, q0, k0);
+          load_b(s + 4 * S, q0, k0);
+          apply(s + S, q1, k1);
+          load_b(s + 5 * S, q1, k1);
+          apply(s + 2 * S, q2, k2);
+          load_b(s + 6 * S, q2, k2);
+          apply(s + 3 * S, q3, k3);
+          load_b(s + 7 * S, q3, k3);
+        }
+      }
+    }
+  }
+
+  if (ksplit > 1) {
+    // this range's float32 tile, in the accumulators' order
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        part[part_index(ks, n_tiles, nt, wave, mb, g, lane)] =
+            make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+    return;
+  }
+  // one range: round once and write four columns per lane and group (rows in their original order)
+#pragma unroll
+  for (int mb = 0; mb < kDMB; ++mb) {
+    const int row = R0 + mb * 32 + (lane & 31);
+    if (row >= T) continue;
+    const int64_t orig = d_orig[row];
+    const int64_t lq = d_last[row];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = cw0 + g * 8 + (lane >> 5) * 4;
+      if (col >= n_out) continue;
+      const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
+      const uint32_t hi = pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+      if (vec && col + 3 < n_out) {
+        *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
+        if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * n_out + col) = make_uint2(lo, hi);
+      } else {
+        const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+        for (int e = 0; e < 4 && col + e < n_out; ++e) {
+          y[orig * y_stride + col + e] = h[e];
+          if (lq >= 0) last_out[lq * n_out + col + e] = h[e];
+        }
+      }
+    }
+  }
+}
+
+// Second launch of a split decode product: thread f takes float4 f of every range's partial tiles (the same position
+// in each), adds the ranges in order, rounds once and writes its row's four columns.
+__global__ __launch_bounds__(kDRedThreads) void dec_reduce_kernel(const float4* __restrict__ part, int32_t ksplit,
+                                                                  int32_t n_tiles, mlora_route_t r,
+                                                                  uint16_t* __restrict__ y, int64_t y_stride,
+                                                                  uint16_t* __restrict__ last_out, int32_t n_out,
+                                                                  int32_t vec) {
+  const int64_t per = (int64_t)n_tiles * 8 * kDMB * 4 * 64;  // float4s per range
+  const int64_t f = (int64_t)blockIdx.x * kDRedThreads + threadIdx.x;
+  if (f >= per) return;
+  const int lane = (int)(f & 63);
+  const int64_t q = f >> 6;
+  const int g = (int)(q & 3), mb = (int)((q >> 2) % kDMB);
+  const int64_t wt = (q >> 2) / kDMB;
+  const int wave = (int)(wt % 8), nt = (int)(wt / 8);
+  const int row = (wave / kDCG) * 32 * kDMB + mb * 32 + (lane & 31);
+  const int col = nt * kDCols + (wave % kDCG) * 32 + g * 8 + (lane >> 5) * 4;
+  if (row >= r.tokens || col >= n_out) return;
+  float4 v = part[f];
+  for (int ks = 1; ks < ksplit; ++ks) {
+    const float4 u = part[(int64_t)ks * per + f];
+    v.x += u.x;
+    v.y += u.y;
+    v.z += u.z;
+    v.w += u.w;
+  }
+  const uint32_t lo = pack_bf16x2(v.x, v.y), hi = pack_bf16x2(v.z, v.w);
+  const int64_t orig = r.tok_perm[row];
+  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
+  if (vec && col + 3 < n_out) {
+    *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
+    if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * n_out + col) = make_uint2(lo, hi);
+  } else {
+    const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+    for (int e = 0; e < 4 && col + e < n_out; ++e) {
+      y[orig * y_stride + col + e] = h[e];
+      if (lq >= 0) last_out[lq * n_out + col + e] = h[e];
+    }
+  }
+}
+
+}  // namespace
+
+size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit) {
+  if (ksplit <= 1) return 0;
+  return (size_t)ksplit * (size_t)(w.columns / kDCols) * kDRows * kDCols * 4;
+}
+
+int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
+               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
+  if (r.tokens == 0 || n_out == 0) return MLORA_OK;
+  if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit) return MLORA_EINVAL;
+  if (ksplit > 1 && part == nullptr) return MLORA_EWORKSPACE;
+  const int n_tiles = w.columns / kDCols;
+  // 8-byte stores of four columns need 8-byte aligned output rows
+  const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
+                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0));
+  float4* p4 = reinterpret_cast<float4*>(part);
+  hipLaunchKernelGGL(dec_kernel, dim3((unsigned)(n_tiles * ksplit)), dim3(kDThreads), 0, stream, w, L, r, x, x_stride,
+                     y, y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, p4, ksplit);
+  if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
+  if (ksplit > 1) {
+    const int64_t per = (int64_t)n_tiles * kDRows * kDCols / 4;
+    hipLaunchKernelGGL(dec_reduce_kernel, dim3((unsigned)((per + kDRedThreads - 1) / kDRedThreads)),
+                       dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, n_out,
+                       (int32_t)vec);
+    if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
+  }
+  return MLORA_OK;
+}

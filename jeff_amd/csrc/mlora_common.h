@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <climits>
 #include <stdint.h>
 
 #include "jeff_mlora.h"
@@ -161,6 +162,12 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                   hipStream_t stream);
+// Narrow product (every token, at most 256, in one row tile of 64 columns): ksplit input ranges; with ksplit > 1
+// part holds dec_partials_bytes(w, ksplit) and a second launch adds the ranges.
+size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit);
+int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
+               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

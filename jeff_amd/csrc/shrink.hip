@@ -9,6 +9,7 @@
 //    the x rows through per-wave LDS rings and A into registers one chunk ahead, and add their partial sums in a
 //    fixed order.
 #include "shrink_seg.h"
+#include "tile_common.h"
 
 namespace {
 
@@ -20,13 +21,9 @@ constexpr int kSBlocks = 2;   // 32-rank blocks per pass
 constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
 constexpr int kSLoads = 4 + 4 * kSBlocks;  // memory instructions per chunk and lane: x rows to LDS, then A
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Per-wave rings of two x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
 __shared__ __attribute__((aligned(16))) uint16_t s_ring0[kSWaves * kSRows * kSChunk];
 __shared__ __attribute__((aligned(16))) uint16_t s_ring1[kSWaves * kSRows * kSChunk];
-
-#define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
 
 // Long segments (prefill): one workgroup per 32 sorted rows; its 4 waves split the input dimension into chunks of
 // 64. A wave streams its chunks of the 32 x rows (gathered through the sorted order) into its own LDS ring with

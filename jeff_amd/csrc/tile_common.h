@@ -1,0 +1,54 @@
+// Pieces shared by the MFMA tile kernels that stage x in LDS (gemm256.hip, decode.hip, shrink.hip): the swizzled
+// 64-input LDS row layout, the explicit memory waits and barriers of their K loops, the XCD-aware block order and a
+// lane's per-step weight registers.
+#pragma once
+
+#include "mlora_common.h"
+
+namespace mlora {
+
+constexpr int kTK = 64;  // inputs per K step (one 128-byte LDS row of bf16)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Element offset of 16-byte chunk c of row `row` in a swizzled 64-element-per-row tile: the eight chunks of a row
+// are XOR-permuted by (row & 7), so the 16-byte reads of 8 consecutive rows at one logical chunk hit all banks once.
+__device__ __forceinline__ int swz(int row, int c) { return row * kTK + ((c ^ (row & 7)) << 3); }
+
+// Wait until at most n vector memory instructions of this wave are outstanding and its LDS operations are done
+// (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
+#define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+
+// Workgroup barrier that orders LDS accesses only (global stores in flight are not waited for).
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Step barrier of a K loop where LDS is written only by the x loads and only read by the waves. The wave's own x
+// loads of the next step have landed (MLORA_WAIT_VM before this); its LDS reads are drained inside the asm
+// statement, so none can be scheduled between the drain and the barrier; then the barrier. There is no release fence:
+// a fence would also wait for the x loads in flight for two steps ahead. The memory clobbers keep the compiler from
+// moving LDS reads or loads across the barrier.
+__device__ __forceinline__ void step_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// blockIdx -> tile index such that consecutive tiles share an XCD (blocks are dealt to the 8 XCDs round-robin)
+__device__ __forceinline__ int xcd_tile(int b, int nb) {
+  const int per = nb / 8, extra = nb % 8;
+  const int xcd = b % 8, slot = b / 8;
+  return xcd * per + min(xcd, extra) + slot;
+}
+
+// One step's weights as loaded by a lane: word [k16] of its column, and the raw bf16 scale and zero point of its
+// column (converted only when used, a step later)
+struct WStage {
+  uint32_t w[4];
+  uint32_t sbits, zbyte;
+};
+
+}  // namespace mlora

@@ -46,8 +46,11 @@ def test_header_constants_match_the_binding() -> None:
     assert const("MLORA_ROUTE_BAD_SEQLENS") == _lib.ROUTE_BAD_SEQLENS
     for name, value in (("MLORA_FORCE_BASE_GEMV", _lib.FORCE_BASE_GEMV), ("MLORA_FORCE_BASE_MFMA", _lib.FORCE_BASE_MFMA),
                         ("MLORA_FORCE_SHRINK_SEGMENT", _lib.FORCE_SHRINK_SEGMENT),
-                        ("MLORA_FORCE_SHRINK_MFMA", _lib.FORCE_SHRINK_MFMA)):
+                        ("MLORA_FORCE_SHRINK_MFMA", _lib.FORCE_SHRINK_MFMA),
+                        ("MLORA_FORCE_BASE_SPLIT", _lib.FORCE_BASE_SPLIT),
+                        ("MLORA_FORCE_BASE_NARROW", _lib.FORCE_BASE_NARROW)):
         assert const(name) == value
+    assert re.search(r"#define MLORA_FORCE_RANGES\(s\) \(\(s\) << 8\)", text) and _lib.force_ranges(4) == 4 << 8
     assert ctypes.sizeof(_lib.Int4) == 8 * 3 + 4 * 4
     assert ctypes.sizeof(_lib.Lora) == 8 * 4 + 8 * 8 + 4 * 4 + 4 * 16
 

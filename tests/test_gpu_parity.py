@@ -200,8 +200,11 @@ def reference_pattern_case(seed: int, group: int, asym: bool):
 @pytest.mark.parametrize("tokens,row_len", [(32, 32), (64, 64), (128, 128), (48, 16), (256, 32), (1024, 64), (4, 1),
                                             (8, 1)])
 @pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "segment"), Int4Tiles("mfma", "mfma"),
-                                   Int4Tiles("split", "segment"), Int4Tiles("split", "mfma")])
+                                   Int4Tiles("split", "segment"), Int4Tiles("split", "mfma"),
+                                   Int4Tiles("narrow", "segment"), Int4Tiles("narrow", "mfma", 2)])
 def test_reference_pattern_products_are_within_the_bound(tokens: int, row_len: int, tiles) -> None:
+    if tiles is not None and tiles.base == "narrow" and tokens > 256:
+        pytest.skip("the narrow product takes at most 256 tokens")
     case = reference_pattern_case(tokens + row_len, 64, False)
     lin = case.lin
     rows = tokens // row_len
@@ -231,7 +234,8 @@ def test_decode_gemv_products(tokens: int, shrink_kind: str) -> None:
 
 
 @pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "mfma"), Int4Tiles("mfma", "segment"),
-                                   Int4Tiles("split", "mfma")])
+                                   Int4Tiles("split", "mfma"), Int4Tiles("split", "segment"),
+                                   Int4Tiles("narrow", "segment", 1), Int4Tiles("narrow", "segment", 8)])
 def test_mixed_rank_decode_batch(tiles) -> None:
     """256 one-token rows, 64 adapters of ranks 8/16/32/64, a qkv-shaped group (2048 -> 2048 + 1024 + 1024)."""
     ranks = {a: [(8, 16, 32, 64)[(a - 1) // 16]] * 3 for a in range(1, 65)}
@@ -242,6 +246,40 @@ def test_mixed_rank_decode_batch(tiles) -> None:
     ws = Workspace(256, 1, max_rank=lin.rank)
     got = int4_product(lin, x, ws, adp, tiles=tiles)
     r = judge(lin, case.w, x, token_ids(adp, lin.pool.shape[0], row_len=1), got)
+    assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
+
+
+NARROW_CASES = {
+    # matrices straddling 32-column groups, a matrix without LoRA, a non-power-of-two capacity, odd ranks
+    "straddle": ([40, 24, 200], 256, [16, 24, 0], {1: [16, 24, 0], 2: [3, 17, 0], 3: [0, 9, 0], 4: [8, 0, 0]}, 37),
+    # capacities above one 64-rank pass (128 and 72), segments longer than a wave's 64 rows
+    "big-cap": ([128, 96], 128, [128, 72], {1: [128, 72], 2: [65, 40], 3: [100, 8]}, 200),
+    # the most tokens, 64 columns only, every token its own request
+    "one-tile": ([64], 512, [32], {a: [(8, 16, 24, 32)[a % 4]] for a in range(1, 33)}, 256),
+    "one-token": ([96, 32], 192, [16, 16], {1: [16, 16], 2: [8, 0]}, 1),
+}
+
+
+@pytest.mark.parametrize("name", list(NARROW_CASES))
+@pytest.mark.parametrize("ranges", [None, 1, 2, 4])
+def test_narrow_products(name: str, ranges) -> None:
+    """The narrow product (every token in one row tile of 64 columns, the LoRA term fused) on awkward groups, with
+    the input dimension in 1, 2 and 4 ranges; each request's last-token row gathered as well."""
+    sizes, k, caps, ranks, tokens = NARROW_CASES[name]
+    if ranges is not None and (k // 64) % ranges:
+        pytest.skip(f"{k // 64} input steps do not split into {ranges} ranges")
+    case = make_case(sizes, k, 128 if k % 128 == 0 else 64, True, ranks, caps, 11)
+    lin = case.lin
+    rng = np.random.default_rng(tokens + k)
+    row_len = 4 if name == "big-cap" else 1
+    requests = tokens // row_len
+    adp = torch.tensor(rng.integers(0, max(ranks) + 1, requests).astype(np.int32), device="cuda")
+    x = torch.randn(tokens, lin.k, device="cuda").to(DT)
+    ws = Workspace(tokens, row_len, max_rank=lin.rank)
+    last = torch.empty(requests, lin.out, dtype=DT, device="cuda")
+    got = int4_product(lin, x, ws, adp, tiles=Int4Tiles("narrow", "segment", ranges), last_out=last)
+    assert torch.equal(last, got[row_len - 1::row_len])
+    r = judge(lin, case.w, x, token_ids(adp, lin.pool.shape[0], row_len=row_len), got)
     assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
 
 
@@ -296,7 +334,8 @@ def test_two_runs_and_a_graph_replay_give_the_same_bits() -> None:
     case = reference_pattern_case(21, 128, True)
     lin = case.lin
     for tokens, row_len, tiles in ((32, 32, None), (1024, 64, None), (6, 1, None), (64, 1, Int4Tiles("mfma", "segment")),
-                                   (64, 1, None), (1024, 64, Int4Tiles("split", "mfma"))):
+                                   (64, 1, None), (1024, 64, Int4Tiles("split", "mfma")),
+                                   (64, 1, Int4Tiles("narrow", "segment", 4)), (256, 4, Int4Tiles("split", "segment"))):
         adp = torch.tensor([CYCLE[r % 4] for r in range(tokens // row_len)], dtype=torch.int32, device="cuda")
         x = torch.randn(tokens, lin.k, device="cuda").to(DT)
         ws = Workspace(tokens, row_len, max_rank=lin.rank)

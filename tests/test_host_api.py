@@ -127,7 +127,9 @@ def test_kernel_layout_round_trips_and_refuses() -> None:
 def test_kernel_choice_rule() -> None:
     assert int4_tiles(4096, 2048, 1) == Int4Tiles("gemv", "segment")
     assert int4_tiles(4096, 2048, 8) == Int4Tiles("gemv", "segment")
-    assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("split", "segment")
+    assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("narrow", "segment")
+    assert int4_tiles(4096, 2048, 257, 257, 65) == Int4Tiles("split", "segment")
+    assert int4_tiles(12288, 2048, 4096, 4096, 1025) == Int4Tiles("split", "segment")
     assert int4_tiles(3072, 1024, 8704, 64, 17) == Int4Tiles("mfma", "mfma")
     with pytest.raises(ValueError):
         int4_tiles(100, 1024, 4)
