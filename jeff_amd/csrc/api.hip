@@ -275,11 +275,12 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
   uint16_t* mid = static_cast<uint16_t*>(workspace);
   const bool mfma_shrink = shrink_on_mfma(route, lora->pool_rows, flags);
   if (base == Base::split && !mfma_shrink) {
-    // split product of short segments: one launch computes the base ranges and, in further workgroups, the first
-    // factor; then the epilogue
+    // split product of short segments: the first factor (its own launch: two of its workgroups fit a CU, where the
+    // base launch's LDS leaves room for one), the base ranges, then the epilogue
     const int32_t ks = split_ranges(w, route->tokens);
     float* part = static_cast<float*>(partials);
-    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s, mid)))
+    if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, false, s))) return rc;
+    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
       return rc;
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
   }

@@ -17,46 +17,51 @@ __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int
 }
 
 constexpr int kDWaves = 8;   // waves per workgroup of the segment form, each a contiguous share of the inputs
-constexpr int kDUnroll = 4;  // 16-input steps per load batch; two batches in flight (120 VGPRs: two workgroups per CU)
+constexpr int kDUnroll = 4;  // 16-input steps per load batch; two batches in flight (two workgroups per CU)
 
-// Short segments (decode): one workgroup per (segment, 32-rank block of the adapter's live ranks). Its 8 waves split
-// the input dimension; a lane streams its rank row of A and its token row of x (the segment's rows as the second
-// MFMA operand, rows past the segment masked to zero) straight into MFMA operands, 8 steps of 16 inputs in flight;
-// one 32x32x16 MFMA per step accumulates a 32-rank x 32-row block. The waves' sums are added in wave order through
-// LDS and rounded once. Segments longer than 32 rows take their rows 32 at a time (A is then re-read from L2).
-// `block` is the workgroup's index among the (segment, rank block) pairs, `red` 32 KB of LDS. Every thread of the
-// workgroup must call it (it synchronises the workgroup).
+// Short segments (decode): one workgroup per (segment, 32-rank block of a matrix's capacity); blocks past the
+// adapter's live rank of that matrix return at once. Its 8 waves split the input dimension; a lane streams its rank
+// row of A and its token row of x (the segment's rows as the second MFMA operand, rows past the segment masked to
+// zero) straight into MFMA operands, 8 steps of 16 inputs in flight; one 32x32x16 MFMA per step accumulates a
+// 32-rank x 32-row block. The waves' sums are added in wave order through LDS and rounded once. Segments longer than
+// 32 rows take their rows 32 at a time (A is then re-read from L2). The block's bookkeeping is read in two dependent
+// rounds (segment bounds and adapter together, then the adapter's rank and the segment's token order) before the
+// A and x loads. `block` is the workgroup's index among the (segment, rank block) pairs, `red` 32 KB of LDS. Every
+// thread of the workgroup must call it (it synchronises the workgroup).
 __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const mlora_route_t& r,
                                                  const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
                                                  uint16_t* __restrict__ mid, int32_t max_blocks, int block,
                                                  float* __restrict__ red) {
-  const int s = block / max_blocks, b = block - s * max_blocks;
-  if (s >= *r.num_segs) return;
-  const int a = r.seg_adapter[s];
-  if (a == 0) return;  // the base row: no first factor is read
-  int rk[MLORA_MAX_MATS];
-  int nblk = 0;
-  for (int j = 0; j < L.n_mats; ++j) {
-    rk[j] = live_rank(L, a, j);
-    nblk += (rk[j] + 31) >> 5;
+  const int s = block / max_blocks;
+  int j = 0, kb = block - s * max_blocks;  // (matrix, 32-rank block) from the capacities
+  while (j + 1 < L.n_mats && kb >= (L.cap[j] + 31) >> 5) {
+    kb -= (L.cap[j] + 31) >> 5;
+    ++j;
   }
-  if (b >= nblk) return;
-  int j = 0, kb = 0;
-  rank_block(rk, L.n_mats, b, j, kb);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (kb * 32 >= L.cap[j]) return;
+  // s < max_segs, so all four reads are inside their arrays
+  const int nseg = *r.num_segs;
+  const int a = r.seg_adapter[s];
+  const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+  if (s >= nseg || a == 0 || se <= sb) return;  // a == 0: the base row, no first factor
+  const int lane = threadIdx.x & 63;
+  const int rk = live_rank(L, a, j);
+  const int32_t tok0 = r.tok_perm[min(sb + (lane & 31), se - 1)];  // the first row block's tokens
+  if (kb * 32 >= rk) return;
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int n = kb * 32 + (lane & 31);  // this lane's rank row
-  const bool aok = n < rk[j];
+  const bool aok = n < rk;
   const uint32_t amask = aok ? 0xFFFFFFFFu : 0u;
   const uint16_t* arow =
       L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rank_offset(L, j) + (aok ? n : 0)) * k + 8 * (lane >> 5);
   const int steps = k / 16;
   const int c0 = (wave * steps) / kDWaves, c1 = ((wave + 1) * steps) / kDWaves;  // this wave's 16-input steps
-  const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
   for (int64_t p0 = sb; p0 < se; p0 += 32) {
     const int64_t prow = p0 + (lane & 31);
     const bool rin = prow < se;
     const uint32_t xmask = rin ? 0xFFFFFFFFu : 0u;
-    const uint16_t* xrow = x + (int64_t)r.tok_perm[rin ? prow : p0] * x_stride + 8 * (lane >> 5);
+    const int32_t tok = p0 == sb ? tok0 : r.tok_perm[rin ? prow : p0];
+    const uint16_t* xrow = x + (int64_t)tok * x_stride + 8 * (lane >> 5);
     f32x16_t acc = f32x16_t{};
     // every load is unconditional (steps past the wave's range re-read its last one and are not multiplied)
     uint4 av[2][kDUnroll], xv[2][kDUnroll];
@@ -98,7 +103,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
       for (int w = 1; w < kDWaves; ++w) sum += red[(w * 16 + i) * kWave + ln];
       const int q = kb * 32 + (i >> 2) * 8 + (ln >> 5) * 4 + (i & 3);
       const int64_t p = p0 + (ln & 31);
-      if (q < rk[j] && p < se) mid[p * L.rank_cap + rank_offset(L, j) + q] = f32_to_bf16(sum);
+      if (q < rk && p < se) mid[p * L.rank_cap + rank_offset(L, j) + q] = f32_to_bf16(sum);
     }
   }
 }
