@@ -143,8 +143,8 @@ def main() -> int:
     tokens_per_s = w.tokens / (ms_per_step / 1e3)
 
     # the dominant kernel alone: the base product and the LoRA second factor of the largest group of layer 0 (one
-    # launch of the fused 256-tile kernel for prefill; for decode the split product's two launches), timed with HIP
-    # events on the stream it runs on (the first factors it reads are computed once beforehand)
+    # launch of the fused 256-tile kernel for prefill; for decode the narrow or split product's launches), timed with
+    # HIP events on the stream it runs on (the first factors it reads are computed once beforehand)
     label = DOMINANT[args.workload]
     lin = w.layers[0][label]
     x = xs[(0, label)]
@@ -192,6 +192,7 @@ def main() -> int:
     kernel = {"mfma": "base_mfma256_kernel (INT4 base + fused LoRA expand)" if w.tokens >= 1024 else
               "base_mfma_kernel<true> (INT4 base + fused LoRA expand)",
               "split": "base_mfma256_kernel, split mode + finish_kernel (INT4 base + LoRA expand, 2 launches)",
+              "narrow": "dec_kernel (INT4 base + fused LoRA expand; dec_reduce_kernel adds split input ranges)",
               "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[tiles.base]
     roof.update({"kernel": kernel, "group": f"layer0.{label}", "launch_ms": kms, "flops_per_launch": kflops,
                  "bytes_per_launch": kbytes})

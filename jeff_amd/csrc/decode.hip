@@ -12,8 +12,9 @@
 // dec_reduce_kernel adds the ranges in order and rounds once.
 // LoRA: the first factors of the wave's rows (64 ranks of matrix j) are loaded once; the adapter segments crossing
 // those rows are listed one per lane (adapter, live rank), and their sB operands stream from memory four segments
-// ahead of the MFMAs (with S input ranges, range ks takes every S-th of the wave's segments from the ks-th). A segment's term goes into the row blocks it crosses, with the first
-// factors of rows outside the segment, and ranks past its live rank, set to zero.
+// ahead of the MFMAs (with S input ranges, range ks takes every S-th of the wave's segments from the ks-th). A
+// segment's term goes into the row blocks it crosses, with the first factors of rows outside the segment, and ranks
+// past its live rank, set to zero.
 #include <type_traits>
 
 #include "tile_common.h"
