@@ -25,7 +25,6 @@
 // the single rounding to bf16, staged through LDS so every output row is written in whole 512-byte pieces.
 #include <type_traits>
 
-#include "shrink_seg.h"
 #include "tile_common.h"
 
 namespace {
@@ -51,15 +50,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                                uint16_t* __restrict__ y, int64_t y_stride,
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
                                                                const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec,
-                                                               float* __restrict__ part, int32_t ksplit, int32_t base_blocks,
-                                                               uint16_t* __restrict__ smid, int32_t s_max_blocks) {
-  if ((int)blockIdx.x >= base_blocks) {
-    // a split launch's extra workgroups: the LoRA first factor of the short segments (the base ranges only read x
-    // and write their partial sums, so the two kinds of work are independent)
-    shrink_seg_block(L, r, x, x_stride, w.k, smid, s_max_blocks, blockIdx.x - base_blocks,
-                     reinterpret_cast<float*>(g_x0));
-    return;
-  }
+                                                               float* __restrict__ part, int32_t ksplit,
+                                                               int32_t base_blocks) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
   // Block b -> (K range ks, row tile mt, column tile nt), column tiles innermost: the blocks that share x rows (one
@@ -385,12 +377,8 @@ int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
 
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, uint16_t* smid) {
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
-  // a split launch may also compute the first factor into smid, in workgroups after the base ranges
-  int s_max_blocks = 0;
-  for (int j = 0; smid != nullptr && j < L.n_mats; ++j) s_max_blocks += (L.cap[j] + 31) / 32;
-  const int64_t s_blocks = smid != nullptr ? (int64_t)r.max_segs * s_max_blocks : 0;
   const int n_tiles = (n_out + kTN - 1) / kTN;
   const int mb = tile_blocks(r.tokens, n_tiles, ksplit);
   const int m_tiles = (int)((r.tokens + 32 * mb - 1) / (32 * mb));
@@ -398,12 +386,12 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);
-  const dim3 grid((unsigned)(blocks + s_blocks));
+  const dim3 grid((unsigned)blocks);
   if (mb == 7)
     hipLaunchKernelGGL(base_mfma256_kernel<7>, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride,
-                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks, smid, s_max_blocks);
+                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks);
   else
     hipLaunchKernelGGL(base_mfma256_kernel<8>, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride,
-                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks, smid, s_max_blocks);
+                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

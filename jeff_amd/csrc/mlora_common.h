@@ -157,7 +157,7 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
 // 256 x 256 tiles; with part != nullptr the split mode: ksplit input ranges, float32 sums to part, nothing else.
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, uint16_t* smid = nullptr);
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream);
 // The second launch of a split product: partial sums in order + LoRA term, rounded once.
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,

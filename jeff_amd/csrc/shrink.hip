@@ -164,8 +164,8 @@ __global__ __launch_bounds__(kDWaves * 64) void shrink_seg_kernel(mlora_lora_t L
                                                                  const uint16_t* __restrict__ x, int64_t x_stride,
                                                                  int32_t k, uint16_t* __restrict__ mid,
                                                                  int32_t max_blocks) {
-  __shared__ float red[kDWaves * 16 * kWave];
-  shrink_seg_block(L, r, x, x_stride, k, mid, max_blocks, blockIdx.x, red);
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kSegLds];
+  shrink_seg_block(L, r, x, x_stride, k, mid, max_blocks, blockIdx.x, lds);
 }
 
 }  // namespace

@@ -1,8 +1,8 @@
-// The LoRA first factor for short segments (decode), shared by its own kernel (shrink.hip) and by the split
-// product's first launch (gemm256.hip), whose extra workgroups compute it beside the base product's ranges.
+// The LoRA first factor for short segments (decode): the segment form of the shrink (shrink.hip's
+// shrink_seg_kernel).
 #pragma once
 
-#include "mlora_common.h"
+#include "tile_common.h"
 
 namespace mlora {
 
@@ -16,22 +16,25 @@ __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int
   kb = b;
 }
 
-constexpr int kDWaves = 8;   // waves per workgroup of the segment form, each a contiguous share of the inputs
-constexpr int kDUnroll = 4;  // 16-input steps per load batch; two batches in flight (two workgroups per CU)
+constexpr int kDWaves = 8;                // waves per workgroup of the segment form, each a share of the inputs
+constexpr int kDChunk = 64;               // inputs per staged chunk of A (32 rank rows of 128 bytes)
+constexpr int kSegLds = kDWaves * 2 * 32 * kDChunk;  // bf16 elements of LDS: two chunk buffers per wave
 
 // Short segments (decode): one workgroup per (segment, 32-rank block of a matrix's capacity); blocks past the
-// adapter's live rank of that matrix return at once. Its 8 waves split the input dimension; a lane streams its rank
-// row of A and its token row of x (the segment's rows as the second MFMA operand, rows past the segment masked to
-// zero) straight into MFMA operands, 8 steps of 16 inputs in flight; one 32x32x16 MFMA per step accumulates a
-// 32-rank x 32-row block. The waves' sums are added in wave order through LDS and rounded once. Segments longer than
-// 32 rows take their rows 32 at a time (A is then re-read from L2). The block's bookkeeping is read in two dependent
-// rounds (segment bounds and adapter together, then the adapter's rank and the segment's token order) before the
-// A and x loads. `block` is the workgroup's index among the (segment, rank block) pairs, `red` 32 KB of LDS. Every
-// thread of the workgroup must call it (it synchronises the workgroup).
+// adapter's live rank of that matrix return at once. Its 8 waves split the input dimension into chunks of 64. A wave
+// stages each chunk of its 32 rank rows of A in its own two LDS buffers with buffer loads that write LDS directly
+// (an instruction covers 8 whole 128-byte rows: every cache line it touches is used whole), one chunk ahead, and
+// loads its token rows of x for the chunk into registers (the segment's rows as the second MFMA operand, rows past
+// the segment masked to zero); one 32x32x16 MFMA per 16 inputs accumulates a 32-rank x 32-row block. The waves'
+// sums are then added in wave order through LDS and rounded once. Segments longer than 32 rows take their rows 32 at
+// a time (A is then re-read from L2). The block's bookkeeping is read in two dependent rounds (segment bounds and
+// adapter together, then the adapter's rank and the segment's token order) before the A and x loads. `block` is the
+// workgroup's index among the (segment, rank block) pairs, `lds` kSegLds elements of LDS. Every thread of the
+// workgroup must call it (it synchronises the workgroup).
 __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const mlora_route_t& r,
-                                                 const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
+                                                 const uint16_t* x, int64_t x_stride, int32_t k,
                                                  uint16_t* __restrict__ mid, int32_t max_blocks, int block,
-                                                 float* __restrict__ red) {
+                                                 uint16_t* __restrict__ lds) {
   const int s = block / max_blocks;
   int j = 0, kb = block - s * max_blocks;  // (matrix, 32-rank block) from the capacities
   while (j + 1 < L.n_mats && kb >= (L.cap[j] + 31) >> 5) {
@@ -48,14 +51,34 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
   const int rk = live_rank(L, a, j);
   const int32_t tok0 = r.tok_perm[min(sb + (lane & 31), se - 1)];  // the first row block's tokens
   if (kb * 32 >= rk) return;
-  const int tid = threadIdx.x, wave = tid >> 6;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = kb * 32 + (lane & 31);  // this lane's rank row
-  const bool aok = n < rk;
-  const uint32_t amask = aok ? 0xFFFFFFFFu : 0u;
-  const uint16_t* arow =
-      L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rank_offset(L, j) + (aok ? n : 0)) * k + 8 * (lane >> 5);
-  const int steps = k / 16;
-  const int c0 = (wave * steps) / kDWaves, c1 = ((wave + 1) * steps) / kDWaves;  // this wave's 16-input steps
+  const uint32_t amask = n < rk ? 0xFFFFFFFFu : 0u;
+  // A rows rho_j + 32 kb .. +31 of the adapter through a buffer resource based at the block (rows past the live rank
+  // re-read the block's first row). DMA instruction i fills rows 8 i + (lane >> 3): lane l writes LDS slot l & 7 of
+  // its row, which holds 16-byte chunk (l & 7) ^ (row & 7) of the row's 64 inputs.
+  const uint16_t* ablk = L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rank_offset(L, j) + kb * 32) * k;
+  const __amdgpu_buffer_rsrc_t ares =
+      __builtin_amdgcn_make_buffer_rsrc((void*)ablk, (short)0, (int)(32 * k * 2), 0x00020000);
+  const int live_rows = min(rk - kb * 32, 32);
+  uint32_t aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    aoff[i] = (uint32_t)(((row < live_rows ? row : 0) * k + (((lane & 7) ^ (row & 7)) << 3)) * 2);
+  }
+  uint16_t* buf0 = lds + wave * (2 * 32 * kDChunk);
+  uint16_t* buf1 = buf0 + 32 * kDChunk;
+  auto dma_a = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(buf + i * 8 * kDChunk), 16, aoff[i], kc * 2, 0, 0);
+  };
+  const int chunks = k / kDChunk;
+  const int ch0 = (wave * chunks) / kDWaves, ch1 = ((wave + 1) * chunks) / kDWaves;  // this wave's chunks
+  float* red = reinterpret_cast<float*>(lds);
   for (int64_t p0 = sb; p0 < se; p0 += 32) {
     const int64_t prow = p0 + (lane & 31);
     const bool rin = prow < se;
@@ -63,36 +86,50 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
     const int32_t tok = p0 == sb ? tok0 : r.tok_perm[rin ? prow : p0];
     const uint16_t* xrow = x + (int64_t)tok * x_stride + 8 * (lane >> 5);
     f32x16_t acc = f32x16_t{};
-    // every load is unconditional (steps past the wave's range re-read its last one and are not multiplied)
-    uint4 av[2][kDUnroll], xv[2][kDUnroll];
-    auto issue = [&](uint4 (&aq)[kDUnroll], uint4 (&xq)[kDUnroll], int c) __attribute__((always_inline)) {
+    auto load_x = [&](uint4 (&xq)[4], int c) __attribute__((always_inline)) {
 #pragma unroll
-      for (int u = 0; u < kDUnroll; ++u) {
-        const int kk = max(min(c + u, c1 - 1), c0) * 16;
-        aq[u] = *reinterpret_cast<const uint4*>(arow + kk);
-        xq[u] = *reinterpret_cast<const uint4*>(xrow + kk);
-      }
+      for (int u = 0; u < 4; ++u) xq[u] = *reinterpret_cast<const uint4*>(xrow + c * kDChunk + 16 * u);
     };
-    auto compute = [&](const uint4 (&aq)[kDUnroll], const uint4 (&xq)[kDUnroll], int c) __attribute__((always_inline)) {
+    // chunk c: A operands from its LDS buffer (row = rank lane & 31, 16-byte chunk 2 u + (lane >> 5)), x from xq
+    // (zero when `live` is false: a chunk past the wave's last, re-read only to keep the loop free of branches)
+    auto compute = [&](const uint16_t* buf, const uint4 (&xq)[4], bool live) __attribute__((always_inline)) {
+      const uint4* bv = reinterpret_cast<const uint4*>(buf);
+      const uint32_t xm4 = live ? xmask : 0u;
+      uint4 av[4];
 #pragma unroll
-      for (int u = 0; u < kDUnroll; ++u) {
-        if (c + u >= c1) break;
-        const uint4 am = make_uint4(aq[u].x & amask, aq[u].y & amask, aq[u].z & amask, aq[u].w & amask);
-        const uint4 xm = make_uint4(xq[u].x & xmask, xq[u].y & xmask, xq[u].z & xmask, xq[u].w & xmask);
+      for (int u = 0; u < 4; ++u) av[u] = bv[swz(lane & 31, 2 * u + (lane >> 5)) >> 3];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint4 am = make_uint4(av[u].x & amask, av[u].y & amask, av[u].z & amask, av[u].w & amask);
+        const uint4 xm = make_uint4(xq[u].x & xm4, xq[u].y & xm4, xq[u].z & xm4, xq[u].w & xm4);
         acc = mfma32(am, xm, acc);
       }
     };
-    if (c1 > c0) {
-      issue(av[0], xv[0], c0);
-      for (int c = c0; c < c1; c += 2 * kDUnroll) {
-        issue(av[1], xv[1], c + kDUnroll);
-        compute(av[0], xv[0], c);
-        if (c + kDUnroll >= c1) break;
-        issue(av[0], xv[0], c + 2 * kDUnroll);
-        compute(av[1], xv[1], c + kDUnroll);
+    if (ch1 > ch0) {
+      // Chunk c + 1's A rows and x are issued before chunk c is used: 8 loads (4 into LDS, 4 into registers) per
+      // chunk, so chunk c has landed when at most 8 are outstanding. The count holds only if no load moves across a
+      // wait: the loop body has no branch (a chunk past the wave's last is re-read and multiplied by zero), x is not
+      // a restrict pointer (so the waits' memory clobbers pin its loads), and scheduling barriers fence the waits.
+      uint4 x0[4], x1[4];
+      dma_a(buf0, ch0 * kDChunk);
+      load_x(x0, ch0);
+      for (int c = ch0; c < ch1; c += 2) {
+        dma_a(buf1, min(c + 1, ch1 - 1) * kDChunk);
+        load_x(x1, min(c + 1, ch1 - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c landed (no LDS read moves above this)
+        __builtin_amdgcn_sched_barrier(0);
+        compute(buf0, x0, true);
+        dma_a(buf0, min(c + 2, ch1 - 1) * kDChunk);
+        load_x(x0, min(c + 2, ch1 - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c + 1 landed
+        __builtin_amdgcn_sched_barrier(0);
+        compute(buf1, x1, c + 1 < ch1);
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last re-reads into LDS have landed
     }
-    __syncthreads();  // the previous row block's sums are read
+    __syncthreads();  // every wave is done with its LDS buffers (and the previous row block's sums are read)
 #pragma unroll
     for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc[i];
     __syncthreads();
@@ -105,6 +142,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
       const int64_t p = p0 + (ln & 31);
       if (q < rk && p < se) mid[p * L.rank_cap + rank_offset(L, j) + q] = f32_to_bf16(sum);
     }
+    __syncthreads();  // the sums are read before the next row block's A chunks overwrite them
   }
 }
 
