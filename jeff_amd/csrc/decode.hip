@@ -6,7 +6,8 @@
 // rows x 32 columns (two 32x32 MFMA blocks). A step's packed words are loaded and dequantised once for the
 // workgroup (one word per thread) into an LDS buffer that every wave reads its weight operands from, and each wave
 // reads its 64 rows of x from an LDS ring that buffer loads with the LDS flag fill, as in the prefill kernel; words
-// and x rows are loaded three steps ahead.
+// and x rows are loaded three steps ahead, and the step's barrier sits in its middle, so the operand reads of each
+// half of a step overlap the other half's MFMAs.
 // When the columns alone are too few for the CUs, the input dimension is split into S ranges: each range writes its
 // float32 tile in the accumulators' own order (one coalesced 1 KB store per MFMA block and column group), and
 // dec_reduce_kernel adds the ranges in order and rounds once.
@@ -150,17 +151,20 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     for (int mb = 0; mb < kDMB; ++mb) a[mb] = xv[swz(R0 + mb * 32 + (lane & 31), c) >> 3];
   };
   // the wave's weight operand for 16 inputs k16: chunk (2 k16 + (lane >> 5)) * 64 + 32 cg + (lane & 31)
+  // (an index the compiler cannot split, so each read's address is one offset from the buffer's start: the compiler
+  // then knows which LDS array the read touches and does not wait for the x loads in flight into the x buffers)
+  int wl = (lane >> 5) * kDCols + cg * 32 + (lane & 31);
+  asm("" : "+v"(wl));
   auto load_w = [&](const uint4* wb, int k16) __attribute__((always_inline)) {
-    return wb[(2 * k16 + (lane >> 5)) * kDCols + cg * 32 + (lane & 31)];
+    return wb[wl + 2 * k16 * kDCols];
   };
-  // A step's operands, all read from LDS before its MFMAs (8 MFMAs per wave are too few to hide a read's latency one
-  // 16-input slice at a time).
-  auto read_ops = [&](const uint16_t* xs, const uint4* wb, uint4 (&a)[kTK / 16][kDMB], uint4 (&b)[kTK / 16])
+  // operands of the 16-input slices k16 = h, h + 1 of a step (h = 0: the first half, h = 2: the second)
+  auto read_half = [&](const uint16_t* xs, const uint4* wb, int h, uint4 (&a)[2][kDMB], uint4 (&b)[2])
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int k16 = 0; k16 < kTK / 16; ++k16) {
-      load_a(xs, k16, a[k16]);
-      b[k16] = load_w(wb, k16);
+    for (int u = 0; u < 2; ++u) {
+      load_a(xs, h + u, a[u]);
+      b[u] = load_w(wb, h + u);
     }
   };
   auto mfma_k16 = [&](const uint4 (&a)[kDMB], const uint4& b) __attribute__((always_inline)) {
@@ -217,29 +221,38 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
   dequant_to(d_w0, s0);
   step_sync();
+  uint4 a01[2][kDMB], b01[2];  // the first half of the current step's operands, read after the previous barrier
+  read_half(d_x0, d_w0, 0, a01, b01);
+  // One barrier per step, in its middle: the second half of step i's operands is read while the first half's MFMAs
+  // run, and the first half of step i + 1's after the barrier, while the second half's MFMAs run. Before the barrier
+  // the wave issues step i + 3's loads (words before x rows: loads complete in order) and dequantises step i + 1's
+  // words into the weight buffer step i - 1 read; the barrier then makes step i + 1's x rows and weights visible.
   auto run = [&](auto slot, int i) __attribute__((always_inline)) {
     constexpr int B = decltype(slot)::value;
     const uint16_t* xs = B == 0 ? d_x0 : B == 1 ? d_x1 : B == 2 ? d_x2 : d_x3;
-    uint16_t* xf = B == 0 ? d_x3 : B == 1 ? d_x0 : B == 2 ? d_x1 : d_x2;  // buffer (i + 3) % 4
-    WStage& wn = B == 0 ? s1 : B == 1 ? s2 : B == 2 ? s3 : s0;            // step i + 1's words
-    WStage& wf = B == 0 ? s3 : B == 1 ? s0 : B == 2 ? s1 : s2;            // step i + 3's words (fetched now)
-    // The step's MFMAs go in between the loads for step i + 3 (words before x rows: loads complete in order) and
-    // the dequantisation of step i + 1's words into the weight buffer step i - 1 read, so the matrix core works
-    // while the wave issues them; the scheduling barriers keep that order.
-    uint4 a[kTK / 16][kDMB], b[kTK / 16];
-    read_ops(xs, (B & 1) ? d_w1 : d_w0, a, b);
-    mfma_k16(a[0], b[0]);
+    const uint16_t* xn = B == 0 ? d_x1 : B == 1 ? d_x2 : B == 2 ? d_x3 : d_x0;  // buffer (i + 1) % 4
+    uint16_t* xf = B == 0 ? d_x3 : B == 1 ? d_x0 : B == 2 ? d_x1 : d_x2;        // buffer (i + 3) % 4
+    WStage& wn = B == 0 ? s1 : B == 1 ? s2 : B == 2 ? s3 : s0;                  // step i + 1's words
+    WStage& wf = B == 0 ? s3 : B == 1 ? s0 : B == 2 ? s1 : s2;                  // step i + 3's words (fetched now)
+    const uint4* wcur = (B & 1) ? d_w1 : d_w0;
+    uint4* wnext = (B & 1) ? d_w0 : d_w1;
+    uint4 a23[2][kDMB], b23[2];
+    read_half(xs, wcur, 2, a23, b23);
+    mfma_k16(a01[0], b01[0]);
     fetch_w(wf, kbase + min(i + 3, nk - 1) * kTK);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_k16(a[1], b[1]);
+    mfma_k16(a01[1], b01[1]);
     dma_x(xf, kbase + min(i + 3, nk - 1) * kTK);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_k16(a[2], b[2]);
-    dequant_to((B & 1) ? d_w0 : d_w1, wn);
-    mfma_k16(a[3], b[3]);
-    // landed: step i + 1's x rows and step i + 2's words (step i + 2's x rows and step i + 3's loads in flight)
-    MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
+    // landed: step i + 1's words and x rows (step i + 2's and i + 3's loads in flight)
+    MLORA_WAIT_VM(kDWLoads + kDXLoads + kDWLoads + kDXLoads);
+    __builtin_amdgcn_sched_barrier(0);
+    dequant_to(wnext, wn);
     step_sync();
+    read_half(xn, wnext, 0, a01, b01);  // past the last step: re-reads of valid buffers, unused
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_k16(a23[0], b23[0]);
+    mfma_k16(a23[1], b23[1]);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;

@@ -132,37 +132,44 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) a[mb] = xv[swz(mb * 32 + (lane & 31), c) >> 3];
   };
-  // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. The A
-  // reads and the dequantisation of the next 16 inputs are interleaved with the current 16 inputs' MFMAs (one MFMA,
-  // then a few VALU instructions or an LDS read), so the matrix core works while the wave converts.
-  auto step = [&](const uint16_t* xs, const WStage& ws) __attribute__((always_inline)) {
+  // One K step: A operands from the x buffer, B operands dequantised in registers from the step's words. Each A
+  // operand register is reloaded right after its MFMA with the next 16 inputs' operand (it is used again eight MFMAs
+  // later), and the next word's dequantisation is interleaved with the MFMAs (one MFMA, then a few VALU instructions
+  // and an LDS read), so the matrix core works while the wave converts. The step's barrier sits before its last 16
+  // inputs: past it, the wave reloads its A registers with the next step's first operands (buffer xn) while the last
+  // MFMAs run. a holds the step's first A operands on entry.
+  uint4 a[MB];
+  auto step = [&](const uint16_t* xs, const WStage& ws, const uint16_t* xn) __attribute__((always_inline)) {
     const float s0v = bf16_to_f32(ws.sbits);
     const float zv = asym ? (float)ws.zbyte : 8.0f;
     const float sv = colok ? s0v : 0.0f;
     const float zs = colok ? zv * s0v : 0.0f;
-    uint4 a0[MB], a1[MB], b0, b1;
-    load_a(xs, 0, a0);
-    b0 = dequant_word(ws.w[0], sv, zs);
+    uint4 b0 = dequant_word(ws.w[0], sv, zs), b1;
 #pragma unroll
     for (int k16 = 0; k16 < kTK / 16; ++k16) {
-      uint4 (&ca)[MB] = (k16 & 1) ? a1 : a0;
-      uint4 (&na)[MB] = (k16 & 1) ? a0 : a1;
-      uint4& cb = (k16 & 1) ? b1 : b0;
+      const uint4& cb = (k16 & 1) ? b1 : b0;
       uint4& nbv = (k16 & 1) ? b0 : b1;
-      if (k16 + 1 < kTK / 16) {
-        load_a(xs, k16 + 1, na);
-        nbv = dequant_word(ws.w[k16 + 1], sv, zs);
+      if (k16 == kTK / 16 - 1) {
+        __builtin_amdgcn_sched_barrier(0);
+        MLORA_WAIT_VM(kWLoads + kXLoads);  // x(i + 1) has landed
+        step_sync();
+      }
+      if (k16 + 1 < kTK / 16) nbv = dequant_word(ws.w[k16 + 1], sv, zs);
+      const uint16_t* src = k16 + 1 < kTK / 16 ? xs : xn;
+      const int c = 2 * ((k16 + 1) % (kTK / 16)) + (lane >> 5);
+      const uint4* xv = reinterpret_cast<const uint4*>(src);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        acc[mb] = mfma32(cb, a[mb], acc[mb]);
+        a[mb] = xv[swz(mb * 32 + (lane & 31), c) >> 3];
       }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(cb, ca[mb], acc[mb]);
-      if (k16 + 1 < kTK / 16) {
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-        }
+      for (int i = 0; i < MB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       }
+      __builtin_amdgcn_sched_barrier(0);  // a reload stays eight MFMAs ahead of its use
     }
   };
 
@@ -179,18 +186,18 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
+  load_a(g_x0, 0, a);
   auto run = [&](auto xb, auto wb, int i) __attribute__((always_inline)) {
     constexpr int XB = decltype(xb)::value, WB = decltype(wb)::value;
     const uint16_t* xs = XB == 0 ? g_x0 : XB == 1 ? g_x1 : g_x2;
-    uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;  // buffer (i + 2) % 3
+    const uint16_t* xn = XB == 0 ? g_x1 : XB == 1 ? g_x2 : g_x0;  // buffer (i + 1) % 3
+    uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;        // buffer (i + 2) % 3
     WStage& cur = WB == 0 ? s0 : s1;
     WStage& nxt = WB == 0 ? s1 : s0;
     fetch_w(nxt, kbase + min(i + 1, nk - 1) * kTK);
     __builtin_amdgcn_sched_barrier(0);  // keep every weight load ahead of the x loads
     dma_x(xf, kbase + min(i + 2, nk - 1) * kTK);
-    step(xs, cur);
-    MLORA_WAIT_VM(kWLoads + kXLoads);  // x(i + 1) has landed
-    step_sync();
+    step(xs, cur, xn);  // past the last step, xn holds re-read rows: the reads are unused
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
