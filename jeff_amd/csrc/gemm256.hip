@@ -139,7 +139,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // inputs: past it, the wave reloads its A registers with the next step's first operands (buffer xn) while the last
   // MFMAs run. a holds the step's first A operands on entry.
   uint4 a[MB];
-  auto step = [&](const uint16_t* xs, const WStage& ws, const uint16_t* xn) __attribute__((always_inline)) {
+  auto step = [&](const uint16_t* xs, const WStage& ws, const uint16_t* xn, auto&& loads_w, auto&& loads_x)
+      __attribute__((always_inline)) {
     const float s0v = bf16_to_f32(ws.sbits);
     const float zv = asym ? (float)ws.zbyte : 8.0f;
     const float sv = colok ? s0v : 0.0f;
@@ -155,6 +156,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         step_sync();
       }
       if (k16 + 1 < kTK / 16) nbv = dequant_word(ws.w[k16 + 1], sv, zs);
+      if (k16 == 0) loads_w();
+      if (k16 == 1) loads_x();
       const uint16_t* src = k16 + 1 < kTK / 16 ? xs : xn;
       const int c = 2 * ((k16 + 1) % (kTK / 16)) + (lane >> 5);
       const uint4* xv = reinterpret_cast<const uint4*>(src);
@@ -168,6 +171,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        if ((k16 == 0 && i < kWLoads) || (k16 == 1 && i < kXLoads))
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
       }
       __builtin_amdgcn_sched_barrier(0);  // a reload stays eight MFMAs ahead of its use
     }
@@ -194,10 +199,9 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     uint16_t* xf = XB == 0 ? g_x2 : XB == 1 ? g_x0 : g_x1;        // buffer (i + 2) % 3
     WStage& cur = WB == 0 ? s0 : s1;
     WStage& nxt = WB == 0 ? s1 : s0;
-    fetch_w(nxt, kbase + min(i + 1, nk - 1) * kTK);
-    __builtin_amdgcn_sched_barrier(0);  // keep every weight load ahead of the x loads
-    dma_x(xf, kbase + min(i + 2, nk - 1) * kTK);
-    step(xs, cur, xn);  // past the last step, xn holds re-read rows: the reads are unused
+    // the next step's words among the first 16 inputs' MFMAs, step i + 2's x rows among the second's
+    step(xs, cur, xn, [&]() __attribute__((always_inline)) { fetch_w(nxt, kbase + min(i + 1, nk - 1) * kTK); },
+         [&]() __attribute__((always_inline)) { dma_x(xf, kbase + min(i + 2, nk - 1) * kTK); });
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
