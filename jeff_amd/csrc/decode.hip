@@ -86,12 +86,12 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     d_last[tid] = (mine && last_out != nullptr) ? r.last_of[tid] : -1;
   }
   // x: instruction i of wave `wave` fills rows (8 i + wave) * 8 .. +7; lane l writes LDS chunk slot l & 7 of row
-  // +(l >> 3), which holds logical chunk (l & 7) ^ (l >> 3). Rows past the tokens read row 0 of the pass.
+  // +(l >> 3), which holds logical chunk swz_slot(row, l & 7). Rows past the tokens read row 0 of the pass.
   uint32_t xoff[kDXLoads];
 #pragma unroll
   for (int i = 0; i < kDXLoads; ++i) {
     const int row = (8 * i + wave) * 8 + (lane >> 3);
-    xoff[i] = (uint32_t)(((int64_t)r.tok_perm[row < T ? row : 0] * x_stride + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+    xoff[i] = (uint32_t)(((int64_t)r.tok_perm[row < T ? row : 0] * x_stride + (swz_slot(row, lane & 7) << 3)) * 2);
   }
   auto dma_x = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
 #pragma unroll

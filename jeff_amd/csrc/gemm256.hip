@@ -16,8 +16,8 @@
 // With no LDS stores in the loop, nothing but the x ring is ordered by the step barrier: a bare barrier after an
 // explicit wait for the x rows of the next step (a __syncthreads(), or any release fence, would also wait for the
 // rows two steps ahead).
-// LDS rows are 128 bytes (64 bf16) with their eight 16-byte chunks XOR-swizzled by (row & 7): the 16-byte operand
-// reads of 8 consecutive rows hit 8 distinct chunk positions, i.e. all banks once. The ring buffers are distinct LDS
+// LDS rows are 128 bytes (64 bf16) with their eight 16-byte chunks XOR-swizzled by (row >> 1) & 7 (tile_common.h's
+// swz): the 16-byte operand reads of 16 consecutive rows hit all 64 banks once. The ring buffers are distinct LDS
 // arrays chosen at compile time (the loop is unrolled by six). Tiles are ordered so that the column tiles of one
 // row tile run on the same XCD (its x rows, the larger operand, then come from that XCD's L2).
 // Epilogue: the tile's first factors (sorted rows) are staged in LDS; each adapter segment crossing the tile adds
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       asym ? (void*)w.zeros : (void*)w.scales, (short)0, (int)(groups * w.columns), 0x00020000);
 
   // x: instruction i of wave `wave` fills rows (8 i + wave) * 8 .. +7; lane l writes LDS chunk slot l & 7 of row
-  // +(l >> 3), which holds logical chunk (l & 7) ^ (l >> 3). Rows past the tokens read row 0 of the pass.
+  // +(l >> 3), which holds logical chunk swz_slot(row, l & 7). Rows past the tokens read row 0 of the pass.
   if (tid < kTM) {
     const int64_t p = p0 + tid;
     const bool mine = tid < kRows && p < T;
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   for (int i = 0; i < kXLoads; ++i) {
     const int row = (8 * i + wave) * 8 + (lane >> 3);
     const int64_t p = p0 + row;
-    xoff[i] = (uint32_t)(((int64_t)r.tok_perm[p < T ? p : 0] * x_stride + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+    xoff[i] = (uint32_t)(((int64_t)r.tok_perm[p < T ? p : 0] * x_stride + (swz_slot(row, lane & 7) << 3)) * 2);
   }
   auto dma_x = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
 #pragma unroll
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         for (int i = 0; i < kXLoads; ++i) {
           const int row = (8 * i + wave) * 8 + (lane >> 3);
           const uint32_t off =
-              (uint32_t)(((p0 + row) * L.rank_cap + rho + rc + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+              (uint32_t)(((p0 + row) * L.rank_cap + rho + rc + (swz_slot(row, lane & 7) << 3)) * 2);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)(g_x0 + (8 * i + wave) * 8 * kTK), 16, off, 0, 0,
                                                    0);
         }

@@ -42,13 +42,13 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
   const int nch = k / kSChunk;
   const int c0 = (wave * nch) / kSWaves, c1 = ((wave + 1) * nch) / kSWaves;  // this wave's chunks
   // x staging: instruction i fills rows 8 i .. 8 i + 7 of the wave's ring slot; lane l writes 16-byte slot l & 7 of
-  // row 8 i + (l >> 3), which holds logical chunk (l & 7) ^ (row & 7)
+  // row 8 i + (l >> 3), which holds logical chunk swz_slot(row, l & 7)
   const uint16_t* xsrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 8 * i + (lane >> 3);
     const int64_t p = p0 + row;
-    xsrc[i] = x + (int64_t)r.tok_perm[p < T ? p : p0] * x_stride + 8 * ((lane & 7) ^ (row & 7));
+    xsrc[i] = x + (int64_t)r.tok_perm[p < T ? p : p0] * x_stride + 8 * swz_slot(row, lane & 7);
   }
   uint16_t* const ring0 = s_ring0 + wave * kSRows * kSChunk;
   uint16_t* const ring1 = s_ring1 + wave * kSRows * kSChunk;
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
           uint4 xo[4];  // the chunk's four x operands, read before the first MFMA
 #pragma unroll
           for (int t = 0; t < 4; ++t)
-            xo[t] = *reinterpret_cast<const uint4*>(&slot[orow * kSChunk + (((2 * t + (lane >> 5)) ^ (orow & 7)) << 3)]);
+            xo[t] = *reinterpret_cast<const uint4*>(&slot[swz(orow, 2 * t + (lane >> 5))]);
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const uint4 xv = make_uint4(xo[t].x & xmask, xo[t].y & xmask, xo[t].z & xmask, xo[t].w & xmask);

@@ -57,7 +57,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
   const uint32_t amask = n < rk ? 0xFFFFFFFFu : 0u;
   // A rows rho_j + 32 kb .. +31 of the adapter through a buffer resource based at the block (rows past the live rank
   // re-read the block's first row). DMA instruction i fills rows 8 i + (lane >> 3): lane l writes LDS slot l & 7 of
-  // its row, which holds 16-byte chunk (l & 7) ^ (row & 7) of the row's 64 inputs.
+  // its row, which holds 16-byte chunk swz_slot(row, l & 7) of the row's 64 inputs.
   const uint16_t* ablk = L.pool + (int64_t)a * L.pool_stride + L.off_a + (int64_t)(rank_offset(L, j) + kb * 32) * k;
   const __amdgpu_buffer_rsrc_t ares =
       __builtin_amdgcn_make_buffer_rsrc((void*)ablk, (short)0, (int)(32 * k * 2), 0x00020000);
@@ -66,7 +66,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 8 * i + (lane >> 3);
-    aoff[i] = (uint32_t)(((row < live_rows ? row : 0) * k + (((lane & 7) ^ (row & 7)) << 3)) * 2);
+    aoff[i] = (uint32_t)(((row < live_rows ? row : 0) * k + (swz_slot(row, lane & 7) << 3)) * 2);
   }
   uint16_t* buf0 = lds + wave * (2 * 32 * kDChunk);
   uint16_t* buf1 = buf0 + 32 * kDChunk;

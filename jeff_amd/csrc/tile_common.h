@@ -11,9 +11,13 @@ constexpr int kTK = 64;  // inputs per K step (one 128-byte LDS row of bf16)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Element offset of 16-byte chunk c of row `row` in a swizzled 64-element-per-row tile: the eight chunks of a row
-// are XOR-permuted by (row & 7), so the 16-byte reads of 8 consecutive rows at one logical chunk hit all banks once.
-__device__ __forceinline__ int swz(int row, int c) { return row * kTK + ((c ^ (row & 7)) << 3); }
+// Swizzled 64-element (128-byte) LDS rows. gfx950's LDS has 64 four-byte banks, so rows 2m and 2m + 1 share one
+// 256-byte bank line, and a 16-byte read serves 16 lanes per cycle: the eight 16-byte chunks of a row are
+// XOR-permuted by (row >> 1) & 7, so the reads of 16 consecutive rows at one logical chunk hit all 64 banks once.
+// swz_slot is the slot holding logical chunk c of row `row` (and, the XOR being its own inverse, the logical chunk
+// held in slot c); swz is the element offset of logical chunk c.
+__device__ __forceinline__ int swz_slot(int row, int c) { return c ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int swz(int row, int c) { return row * kTK + (swz_slot(row, c) << 3); }
 
 // Wait until at most n vector memory instructions of this wave are outstanding and its LDS operations are done
 // (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
