@@ -5,9 +5,9 @@
 //  - shrink_seg: few tokens per adapter (decode). One workgroup per (segment, 32-rank block) streams those 32 rows
 //    of A once into MFMA operands, the segment's rows as the other operand; its waves split the inputs and add their
 //    sums in a fixed order. Memory-bound on A.
-//  - shrink_mfma: long segments (prefill). One workgroup per 32 sorted positions; its waves split the inputs, stream
-//    the x rows through per-wave LDS rings and A into registers one chunk ahead, and add their partial sums in a
-//    fixed order.
+//  - shrink_mfma: long segments (prefill). Workgroups per 32 sorted positions; their waves split the inputs, stream
+//    the x rows through per-wave LDS rings two chunks ahead and A into registers one chunk ahead, and add their
+//    partial sums in a fixed order.
 #include "shrink_seg.h"
 #include "tile_common.h"
 
@@ -21,16 +21,19 @@ constexpr int kSBlocks = 2;   // 32-rank blocks per pass
 constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
 constexpr int kSLoads = 4 + 4 * kSBlocks;  // memory instructions per chunk and lane: x rows to LDS, then A
 
-// Per-wave rings of two x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
+// Per-wave rings of three x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
 __shared__ __attribute__((aligned(16))) uint16_t s_ring0[kSWaves * kSRows * kSChunk];
 __shared__ __attribute__((aligned(16))) uint16_t s_ring1[kSWaves * kSRows * kSChunk];
+__shared__ __attribute__((aligned(16))) uint16_t s_ring2[kSWaves * kSRows * kSChunk];
 
-// Long segments (prefill): one workgroup per 32 sorted rows; its 4 waves split the input dimension into chunks of
-// 64. A wave streams its chunks of the 32 x rows (gathered through the sorted order) into its own LDS ring with
-// buffer loads that cover whole 128-byte rows, one chunk ahead, and loads the matching A operands into registers
-// one chunk ahead; one 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's
-// accumulators hold four consecutive ranks of one token. The four partial sums are added in wave order in LDS
-// and rounded once. Rows outside the segment read zero x operands.
+// Long segments (prefill): two workgroups per 32 sorted rows, (block, 0) for the block's first adapter segment and
+// (block, 1) for the rest (none, unless the block crosses a segment boundary), so a crossing block does not take
+// twice as long as the others. A workgroup's 4 waves split the input dimension into chunks of 64. A wave streams its
+// chunks of the 32 x rows (gathered through the sorted order) into its own three-slot LDS ring with loads that cover
+// whole 128-byte rows, two chunks ahead, and loads the matching A operands into registers one chunk ahead; one
+// 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's accumulators hold four
+// consecutive ranks of one token. The four partial sums are added in wave order in LDS and rounded once. Rows
+// outside the segment read zero x operands.
 __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
                                                                   const uint16_t* __restrict__ x, int64_t x_stride,
                                                                   int32_t k, uint16_t* __restrict__ mid) {
@@ -52,8 +55,12 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
   }
   uint16_t* const ring0 = s_ring0 + wave * kSRows * kSChunk;
   uint16_t* const ring1 = s_ring1 + wave * kSRows * kSChunk;
+  uint16_t* const ring2 = s_ring2 + wave * kSRows * kSChunk;
   const int orow = lane & 31;  // the operand row of this lane
-  const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kSRows, T) - 1];
+  const int s_first = r.seg_of[p0], s_last = r.seg_of[min(p0 + kSRows, T) - 1];
+  // workgroup (block, 0) takes the block's first segment, (block, 1) the others, so a block that crosses a segment
+  // boundary is not twice as long as the rest
+  const int s_lo = blockIdx.y == 0 ? s_first : s_first + 1, s_hi = blockIdx.y == 0 ? s_first : s_last;
   for (int s = s_lo; s <= s_hi; ++s) {
     const int a = r.seg_adapter[s];
     if (a == 0) continue;  // the base row: no first factor is read
@@ -87,13 +94,16 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
       for (int bi = 0; bi < kSBlocks; ++bi) amask[bi] = aok[bi] ? 0xFFFFFFFFu : 0u;
       if (c1 > c0) {
         uint4 aq0[4][kSBlocks], aq1[4][kSBlocks];
-        // one chunk's loads: its x rows into a ring slot, its A operands into registers; every load is unconditional
-        // (chunks past the wave's range re-read its last one), so the counts the waits rely on hold on every path
-        auto issue = [&](uint16_t* slot, uint4 (&aq)[4][kSBlocks], int c) {
+        // a chunk's x rows into a ring slot and its A operands into registers; every load is unconditional (chunks
+        // past the wave's range re-read its last one), so the counts the waits rely on hold on every path
+        auto issue_x = [&](uint16_t* slot, int c) {
           const int kc = min(c, c1 - 1) * kSChunk;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             __builtin_amdgcn_global_load_lds(xsrc[i] + kc, (lds_void*)(slot + i * 8 * kSChunk), 16, 0, 0);
+        };
+        auto issue_a = [&](uint4 (&aq)[4][kSBlocks], int c) {
+          const int kc = min(c, c1 - 1) * kSChunk;
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -116,20 +126,33 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
             }
           }
         };
-        issue(ring0, aq0, c0);
-        issue(ring1, aq1, c0 + 1);
-        for (int c = c0; c < c1; c += 2) {
+        // x rows two chunks ahead (three LDS slots), A operands one chunk ahead (two register sets): the loads are
+        // issued x(c + 2), A(c + 1) before chunk c is used, so chunk c has landed when the 4 + 8 loads issued after
+        // A(c) are the only ones outstanding
+        auto sub = [&](uint16_t* xf, uint4 (&an)[4][kSBlocks], const uint16_t* xs, const uint4 (&ac)[4][kSBlocks],
+                       int c) {
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // the previous chunk's LDS reads are done before its slot is refilled
+          issue_x(xf, c + 2);
+          issue_a(an, c + 1);
           MLORA_WAIT_VM(kSLoads);  // chunk c (x rows and A) has landed
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-          compute(ring0, aq0);
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // its LDS reads are done before the slot is refilled
-          issue(ring0, aq0, c + 2);
+          compute(xs, ac);
+        };
+        issue_x(ring0, c0);
+        issue_x(ring1, c0 + 1);
+        issue_a(aq0, c0);
+        for (int c = c0; c < c1; c += 6) {
+          sub(ring2, aq1, ring0, aq0, c);
           if (c + 1 >= c1) break;
-          MLORA_WAIT_VM(kSLoads);
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-          compute(ring1, aq1);
-          __builtin_amdgcn_s_waitcnt(0xC07F);
-          issue(ring1, aq1, c + 3);
+          sub(ring0, aq0, ring1, aq1, c + 1);
+          if (c + 2 >= c1) break;
+          sub(ring1, aq1, ring2, aq0, c + 2);
+          if (c + 3 >= c1) break;
+          sub(ring2, aq0, ring0, aq1, c + 3);
+          if (c + 4 >= c1) break;
+          sub(ring0, aq1, ring1, aq0, c + 4);
+          if (c + 5 >= c1) break;
+          sub(ring1, aq0, ring2, aq1, c + 5);
         }
         MLORA_WAIT_VM(0);
       }
@@ -175,7 +198,7 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
   if (r.tokens == 0 || r.max_segs == 0) return MLORA_OK;
   if (mfma) {
     const int64_t blocks = (r.tokens + kSRows - 1) / kSRows;
-    hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks), dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k,
+    hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks, 2), dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k,
                        mid);
   } else {
     int max_blocks = 0;  // 32-rank blocks of an adapter using every matrix's capacity
