@@ -189,6 +189,25 @@ def test_shrink_within_one_rounding_of_exact(mfma: bool) -> None:
     assert bad == 0, f"{bad} first factors beyond one rounding (worst {worst:.3g} x the bound)"
 
 
+@pytest.mark.parametrize("k", [64, 192, 448, 1600])
+@pytest.mark.parametrize("mfma", [False, True])
+def test_shrink_input_chunk_counts(k: int, mfma: bool) -> None:
+    """Input sizes whose 64-input chunks split unevenly over a workgroup's waves (none, one or a few each, past the
+    prefetch depth or not), with segments that cross 32-row blocks."""
+    case = make_case([192, 64], k, 64, True, {1: [8, 16], 2: [32, 0], 3: [16, 24]}, [32, 32], 5 + k)
+    rng = np.random.default_rng(k)
+    requests, row_len = 12, 13
+    adp = torch.tensor(rng.integers(0, 4, requests).astype(np.int32), device="cuda")
+    x = torch.randn(requests * row_len, k, device="cuda").to(DT)
+    ws = Workspace(requests * row_len, row_len, max_rank=case.lin.rank)
+    mid = shrink(case.lin, x, ws, adp, mfma=mfma).clone()
+    torch.cuda.synchronize()
+    perm = ws.tok_perm[:x.shape[0]].cpu().numpy()
+    tok = token_ids(adp, case.lin.pool.shape[0], row_len=row_len)
+    bad, worst = mid_bound_check(case.lin, x, tok, perm, mid.cpu())
+    assert bad == 0, f"{bad} first factors beyond one rounding (worst {worst:.3g} x the bound)"
+
+
 CYCLE = (1, 2, 0, 3)  # the reference's adapter pattern over request rows (tests/test_int4_kernels_cuda.py:58)
 
 
