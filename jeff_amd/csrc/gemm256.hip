@@ -40,6 +40,7 @@ constexpr int kWLoads = 4 + 2;   // weight loads per lane and step: 4 words, a s
 __shared__ __attribute__((aligned(16))) uint16_t g_x0[kTM * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t g_x1[kTM * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t g_x2[kTM * kTK];
+__shared__ __attribute__((aligned(16))) uint16_t g_x3[kTM * kTK];  // the output tile's staging only
 __shared__ int32_t g_orig[kTM];  // the tile's rows: original token index, -1 past the tokens
 __shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it is, else -1
 
@@ -189,6 +190,26 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   fetch_w(s0, kbase);
   dma_x(g_x0, kbase);
   dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
+  // The LoRA epilogue's bookkeeping, read while the first x rows load (scalar loads, which the vector-memory waits do
+  // not count): the tile's first and last adapter segments, the first two segments' adapters and their live ranks of
+  // the tile's first matrix.
+  const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
+  const int jlo = lora ? matrix_of(L, n0) : 0;
+  int s_lo = 0, s_hi = -1, a_pre[2] = {0, 0}, live_pre[2] = {0, 0};
+  if (lora) {
+    auto sload = [](const int32_t* q, int64_t i) __attribute__((always_inline)) {
+      return ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)q)[i];
+    };
+    s_lo = sload(r.seg_of, p0);
+    s_hi = sload(r.seg_of, min(p0 + kRows, T) - 1);
+    a_pre[0] = sload(r.seg_adapter, s_lo);
+    a_pre[1] = sload(r.seg_adapter, min(s_lo + 1, s_hi));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int rk = a_pre[u] == 0 ? 0 : sload(L.ranks, (int64_t)a_pre[u] * L.ranks_stride + jlo);
+      live_pre[u] = min(max(rk, 0), L.cap[jlo]);
+    }
+  }
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
   load_a(g_x0, 0, a);
@@ -245,12 +266,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // staged in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come
   // straight from memory as MFMA operands (the next segment's issued before the current one's products), and the
   // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
-  // set to zero.
-  if (L.n_mats > 0 && mid != nullptr) {
-    const int s_lo = r.seg_of[p0], s_hi = r.seg_of[min(p0 + kRows, T) - 1];
+  // set to zero. The first two segments' adapters and live ranks of the first matrix were read in the prologue.
+  if (lora) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)(T * L.rank_cap * 2), 0x00020000);
-    const int jlo = matrix_of(L, n0), jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
+    const int jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
     for (int j = jlo; j <= jhi; ++j) {
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
       // the wave's column inside matrix j (others get zero operands)
@@ -270,8 +290,14 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         }
         // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
         auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
-          const int a = r.seg_adapter[s];
-          const int live = a == 0 ? 0 : live_rank(L, a, j);
+          int a, live;
+          if (j == jlo && s - s_lo < 2) {  // read ahead
+            a = a_pre[s - s_lo];
+            live = live_pre[s - s_lo];
+          } else {
+            a = r.seg_adapter[s];
+            live = a == 0 ? 0 : live_rank(L, a, j);
+          }
           rk = min(live - rc, kRankChunk);
           const int sbs = sb_stride(live, capj);  // the adapter's sB row stride (at least 8: capj > rc >= 0)
           const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
@@ -319,49 +345,49 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     }
   }
 
-  // Single rounding to bf16 and the stores, through LDS one half of the tile (128 rows) at a time: lane l holds, for
-  // row mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave
-  // writes its half-tile rows to LDS (columns 0..127 of the tile in g_x0, 128..255 in g_x1, 256-byte rows with their
-  // 16-byte chunks XOR-swizzled by (row & 15)), then every thread reads 16-byte chunks back and writes whole 512-byte
-  // tile rows to the token's output row (and to its request's last-token row).
+  // Single rounding to bf16 and the stores, through LDS (the whole tile at once): lane l holds, for row
+  // mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave
+  // writes its rows to LDS (rows 0..127 in g_x0 and g_x1, rows 128..255 in g_x2 and g_x3, columns 0..127 of the tile
+  // in the first of each pair; 256-byte rows with their 16-byte chunks XOR-swizzled by (row & 15)), then every
+  // thread reads 16-byte chunks back and writes whole 512-byte tile rows to the token's output row (and to its
+  // request's last-token row).
+  lds_sync();  // every wave is done reading LDS
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    lds_sync();  // every wave is done reading LDS
-    {
-      uint16_t* buf = (wave >> 2) ? g_x1 : g_x0;
+    uint16_t* buf = half == 0 ? ((wave >> 2) ? g_x1 : g_x0) : ((wave >> 2) ? g_x3 : g_x2);
 #pragma unroll
-      for (int mq = 0; mq < 4; ++mq)
+    for (int mq = 0; mq < 4; ++mq)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int mb = half * 4 + mq;
-          if (mb >= MB) break;  // a 224-row tile's second half has three blocks
-          const int row = mq * 32 + (lane & 31);
-          const int col = (wave & 3) * 32 + g * 8 + (lane >> 5) * 4;
-          const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
-          const uint32_t hi = pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
-          *reinterpret_cast<uint2*>(&buf[row * 128 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)]) = make_uint2(lo, hi);
-        }
-    }
-    lds_sync();
+      for (int g = 0; g < 4; ++g) {
+        const int mb = half * 4 + mq;
+        if (mb >= MB) break;  // a 224-row tile's second half has three blocks
+        const int row = mq * 32 + (lane & 31);
+        const int col = (wave & 3) * 32 + g * 8 + (lane >> 5) * 4;
+        const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
+        const uint32_t hi = pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+        *reinterpret_cast<uint2*>(&buf[row * 128 + (((col >> 3) ^ (row & 15)) << 3) + (col & 7)]) = make_uint2(lo, hi);
+      }
+  }
+  lds_sync();
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = tid + kThreads * i;
-      const int row = f >> 5, bsel = (f >> 4) & 1, c = f & 15;
-      const int64_t orig = g_orig[half * 128 + row];
-      if (orig < 0) continue;
-      const int64_t lq = g_last[half * 128 + row];
-      const uint4 v = *reinterpret_cast<const uint4*>(&(bsel ? g_x1 : g_x0)[row * 128 + ((c ^ (row & 15)) << 3)]);
-      const int col = n0 + bsel * 128 + c * 8;
-      if (vec && col + 7 < n_out) {
-        *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
-        if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * n_out + col) = v;
-      } else {
-        const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
-        for (int e = 0; e < 8 && col + e < n_out; ++e) {
-          const uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
-          y[orig * y_stride + col + e] = h;
-          if (lq >= 0) last_out[lq * n_out + col + e] = h;
-        }
+  for (int i = 0; i < 16; ++i) {
+    const int f = tid + kThreads * i;
+    const int half = f >> 12, row = (f >> 5) & 127, bsel = (f >> 4) & 1, c = f & 15;
+    const int64_t orig = g_orig[half * 128 + row];
+    if (orig < 0) continue;
+    const int64_t lq = g_last[half * 128 + row];
+    const uint16_t* buf = half == 0 ? (bsel ? g_x1 : g_x0) : (bsel ? g_x3 : g_x2);
+    const uint4 v = *reinterpret_cast<const uint4*>(&buf[row * 128 + ((c ^ (row & 15)) << 3)]);
+    const int col = n0 + bsel * 128 + c * 8;
+    if (vec && col + 7 < n_out) {
+      *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
+      if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * n_out + col) = v;
+    } else {
+      const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
+      for (int e = 0; e < 8 && col + e < n_out; ++e) {
+        const uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
+        y[orig * y_stride + col + e] = h;
+        if (lq >= 0) last_out[lq * n_out + col + e] = h;
       }
     }
   }
