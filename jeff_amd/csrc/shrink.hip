@@ -17,9 +17,7 @@ using namespace mlora;
 
 constexpr int kSRows = 32;    // sorted rows per workgroup
 constexpr int kSWaves = 4;    // waves per workgroup, each a contiguous share of the inputs (two workgroups per CU)
-constexpr int kSBlocks = 2;   // 32-rank blocks per pass
 constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
-constexpr int kSLoads = 4 + 4 * kSBlocks;  // memory instructions per chunk and lane: x rows to LDS, then A
 
 // Per-wave rings of three x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
 __shared__ __attribute__((aligned(16))) uint16_t s_ring0[kSWaves * kSRows * kSChunk];
@@ -34,9 +32,13 @@ __shared__ __attribute__((aligned(16))) uint16_t s_ring2[kSWaves * kSRows * kSCh
 // 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's accumulators hold four
 // consecutive ranks of one token. The four partial sums are added in wave order in LDS and rounded once. Rows
 // outside the segment read zero x operands.
+// KB: 32-rank blocks per pass (1, 2 or 3, chosen by the host from the group's capacities: all of an adapter's blocks
+// in one pass when there are one or three, so no block slot is a masked re-read)
+template <int KB>
 __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
                                                                   const uint16_t* __restrict__ x, int64_t x_stride,
                                                                   int32_t k, uint16_t* __restrict__ mid) {
+  constexpr int kSLoads = 4 + 4 * KB;  // memory instructions per chunk and lane: x rows to LDS, then A
   const int64_t T = r.tokens;
   const int64_t p0 = (int64_t)blockIdx.x * kSRows;
   if (p0 >= T) return;
@@ -73,27 +75,27 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
       nblk += (rk[j] + 31) >> 5;
     }
     const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a + 8 * (lane >> 5);
-    for (int b0 = 0; b0 < nblk; b0 += kSBlocks) {
-      const uint16_t* asrc[kSBlocks];
-      bool aok[kSBlocks];
+    for (int b0 = 0; b0 < nblk; b0 += KB) {
+      const uint16_t* asrc[KB];
+      bool aok[KB];
 #pragma unroll
-      for (int bi = 0; bi < kSBlocks; ++bi) {
+      for (int bi = 0; bi < KB; ++bi) {
         int j = 0, kb = 0;
         rank_block(rk, L.n_mats, min(b0 + bi, nblk - 1), j, kb);
         const int n = kb * 32 + (lane & 31);
         aok[bi] = b0 + bi < nblk && n < rk[j];
         asrc[bi] = Abase + (int64_t)(rank_offset(L, j) + (aok[bi] ? n : 0)) * k;
       }
-      f32x16_t acc[kSBlocks];
+      f32x16_t acc[KB];
 #pragma unroll
-      for (int bi = 0; bi < kSBlocks; ++bi) acc[bi] = f32x16_t{};
+      for (int bi = 0; bi < KB; ++bi) acc[bi] = f32x16_t{};
       // rows outside the segment and rank rows past the live rank multiply as zeros (bit masks, not branches)
       const uint32_t xmask = rin ? 0xFFFFFFFFu : 0u;
-      uint32_t amask[kSBlocks];
+      uint32_t amask[KB];
 #pragma unroll
-      for (int bi = 0; bi < kSBlocks; ++bi) amask[bi] = aok[bi] ? 0xFFFFFFFFu : 0u;
+      for (int bi = 0; bi < KB; ++bi) amask[bi] = aok[bi] ? 0xFFFFFFFFu : 0u;
       if (c1 > c0) {
-        uint4 aq0[4][kSBlocks], aq1[4][kSBlocks];
+        uint4 aq0[4][KB], aq1[4][KB];
         // a chunk's x rows into a ring slot and its A operands into registers; every load is unconditional (chunks
         // past the wave's range re-read its last one), so the counts the waits rely on hold on every path
         auto issue_x = [&](uint16_t* slot, int c) {
@@ -102,15 +104,15 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
           for (int i = 0; i < 4; ++i)
             __builtin_amdgcn_global_load_lds(xsrc[i] + kc, (lds_void*)(slot + i * 8 * kSChunk), 16, 0, 0);
         };
-        auto issue_a = [&](uint4 (&aq)[4][kSBlocks], int c) {
+        auto issue_a = [&](uint4 (&aq)[4][KB], int c) {
           const int kc = min(c, c1 - 1) * kSChunk;
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int bi = 0; bi < kSBlocks; ++bi)
+            for (int bi = 0; bi < KB; ++bi)
               aq[t][bi] = *reinterpret_cast<const uint4*>(asrc[bi] + kc + 16 * t);
         };
-        auto compute = [&](const uint16_t* slot, const uint4 (&aq)[4][kSBlocks]) {
+        auto compute = [&](const uint16_t* slot, const uint4 (&aq)[4][KB]) {
           uint4 xo[4];  // the chunk's four x operands, read before the first MFMA
 #pragma unroll
           for (int t = 0; t < 4; ++t)
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
           for (int t = 0; t < 4; ++t) {
             const uint4 xv = make_uint4(xo[t].x & xmask, xo[t].y & xmask, xo[t].z & xmask, xo[t].w & xmask);
 #pragma unroll
-            for (int bi = 0; bi < kSBlocks; ++bi) {
+            for (int bi = 0; bi < KB; ++bi) {
               const uint4 av = aq[t][bi];
               acc[bi] = mfma32(make_uint4(av.x & amask[bi], av.y & amask[bi], av.z & amask[bi], av.w & amask[bi]), xv,
                                acc[bi]);
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
         // x rows two chunks ahead (three LDS slots), A operands one chunk ahead (two register sets): the loads are
         // issued x(c + 2), A(c + 1) before chunk c is used, so chunk c has landed when the 4 + 8 loads issued after
         // A(c) are the only ones outstanding
-        auto sub = [&](uint16_t* xf, uint4 (&an)[4][kSBlocks], const uint16_t* xs, const uint4 (&ac)[4][kSBlocks],
+        auto sub = [&](uint16_t* xf, uint4 (&an)[4][KB], const uint16_t* xs, const uint4 (&ac)[4][KB],
                        int c) {
           __builtin_amdgcn_s_waitcnt(0xC07F);  // the previous chunk's LDS reads are done before its slot is refilled
           issue_x(xf, c + 2);
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t 
       // the waves' sums in wave order, one 32-rank block at a time through LDS (the rings are free)
       float* red = reinterpret_cast<float*>(s_ring0);  // [wave][register][lane]
 #pragma unroll
-      for (int bi = 0; bi < kSBlocks; ++bi) {
+      for (int bi = 0; bi < KB; ++bi) {
         __syncthreads();  // every wave is done with the rings (and the previous block's sums)
 #pragma unroll
         for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc[bi][i];
@@ -198,8 +200,16 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
   if (r.tokens == 0 || r.max_segs == 0) return MLORA_OK;
   if (mfma) {
     const int64_t blocks = (r.tokens + kSRows - 1) / kSRows;
-    hipLaunchKernelGGL(shrink_mfma_kernel, dim3((unsigned)blocks, 2), dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k,
-                       mid);
+    // blocks per pass: all of an adapter's blocks when that is one or three (every capacity a multiple of 32), else 2
+    int cap_blocks = 0;
+    for (int j = 0; j < L.n_mats; ++j) cap_blocks += (L.cap[j] + 31) / 32;
+    const dim3 grid((unsigned)blocks, 2);
+    if (cap_blocks == 1)
+      hipLaunchKernelGGL(shrink_mfma_kernel<1>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
+    else if (cap_blocks == 3)
+      hipLaunchKernelGGL(shrink_mfma_kernel<3>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
+    else
+      hipLaunchKernelGGL(shrink_mfma_kernel<2>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
   } else {
     int max_blocks = 0;  // 32-rank blocks of an adapter using every matrix's capacity
     for (int j = 0; j < L.n_mats; ++j) max_blocks += (L.cap[j] + 31) / 32;
