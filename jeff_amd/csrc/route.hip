@@ -168,12 +168,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const int32_t* __r
   if (tid == 0) *r.status = status;
 }
 
-// Passes of at most 64 request rows: wave 0 routes them in registers (one request per lane, a bitonic sort of the
-// same keys by lane shuffles, prefix sums by shuffles), with one barrier before every wave writes the tokens. The
-// outputs are the block kernel's, bit for bit.
+// Passes of at most 64 request rows: one workgroup per request. Wave 0 of every workgroup routes all of them in
+// registers (one request per lane, a bitonic sort of the same keys by lane shuffles, prefix sums by shuffles; a few
+// hundred instructions, cheaper than sharing the result between workgroups); workgroup 0 writes the per-request and
+// per-segment outputs, and after one barrier workgroup b writes the tokens of the request at sorted position b, so
+// the token stores spread over as many CUs as there are requests. The outputs are the block kernel's, bit for bit.
 constexpr int kSmallRequests = 64;
+constexpr int kSmallThreads = 256;
 
-__global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_t* __restrict__ adp,
+__global__ __launch_bounds__(kSmallThreads) void route_small_kernel(const int32_t* __restrict__ adp,
                                                                    const int32_t* __restrict__ cu, int32_t row_len,
                                                                    mlora_route_t r, int32_t pool_rows) {
   __shared__ int32_t s_start[kSmallRequests], s_len[kSmallRequests], s_ps[kSmallRequests];
@@ -228,12 +231,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_
     const int pstart = lsum - qlen, seg = fsum - 1;
     const int nseg = __shfl(fsum, 63), total = __shfl(lsum, 63);
     const bool any_bad_adapter = __ballot(bad_a) != 0;  // every lane takes part in the vote
+    const bool lead = blockIdx.x == 0;  // the one workgroup that writes the per-request and per-segment outputs
     if (seq_ok) {
       if (live) {
-        r.req_order[lane] = q;
-        if (first) {
-          r.seg_adapter[seg] = ada;
-          r.seg_start[seg] = pstart;
+        if (lead) {
+          r.req_order[lane] = q;
+          if (first) {
+            r.seg_adapter[seg] = ada;
+            r.seg_start[seg] = pstart;
+          }
         }
         s_start[lane] = qstart;
         s_len[lane] = qlen;
@@ -241,7 +247,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_
         s_seg[lane] = seg;
         s_q[lane] = q;
       }
-      if (lane == 0) {
+      if (lane == 0 && lead) {
         *r.num_segs = nseg;
         r.seg_start[nseg] = total;
         *r.status = any_bad_adapter ? MLORA_ROUTE_BAD_ADAPTER : 0;
@@ -251,12 +257,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_
   }
   __syncthreads();
   if (!s_ok) {  // unusable offsets: identity routing through row 0 (no LoRA), flagged
-    for (int64_t p = tid; p < T; p += kRouteThreads) {
+    for (int64_t p = (int64_t)blockIdx.x * kSmallThreads + tid; p < T; p += (int64_t)gridDim.x * kSmallThreads) {
       r.tok_perm[p] = (int32_t)p;
       r.last_of[p] = -1;
       r.seg_of[p] = 0;
     }
-    for (int i = tid; i < B; i += kRouteThreads) r.req_order[i] = i;
+    if (blockIdx.x != 0) return;
+    for (int i = tid; i < B; i += kSmallThreads) r.req_order[i] = i;
     if (tid == 0) {
       *r.num_segs = 1;
       r.seg_start[0] = 0;
@@ -266,9 +273,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(const int32_
     }
     return;
   }
-  for (int i = wave; i < B; i += kRouteThreads / 64) {  // one request per wave, its tokens across the lanes
+  for (int i = blockIdx.x; i < B; i += gridDim.x) {  // one request per workgroup, its tokens across the threads
     const int start = s_start[i], l = s_len[i], ps = s_ps[i], sg = s_seg[i], q = s_q[i];
-    for (int t = lane; t < l; t += 64) {
+    for (int t = tid; t < l; t += kSmallThreads) {
       r.tok_perm[ps + t] = start + t;
       r.last_of[ps + t] = t == l - 1 ? q : -1;
       r.seg_of[ps + t] = sg;
@@ -293,7 +300,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(mlora_int4_t w, uint16_t* 
 int launch_route(const int32_t* adp, const int32_t* cu, int32_t row_len, const mlora_route_t& r, int32_t pool_rows,
                  hipStream_t stream) {
   if (r.requests <= kSmallRequests)
-    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
+    hipLaunchKernelGGL(route_small_kernel, dim3((unsigned)(r.requests > 1 ? r.requests : 1)), dim3(kSmallThreads), 0, stream, adp,
+                       cu, row_len, r, pool_rows);
   else
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, adp, cu, row_len, r, pool_rows);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
