@@ -61,7 +61,8 @@ def assert_route_equal(ws: Workspace, tokens: int, want: dict, requests: int) ->
 
 
 @pytest.mark.parametrize("case", ["uniform-32", "decode-256", "one-row", "ragged-64", "ragged-65", "zipf-512",
-                                  "empty-rows", "all-base", "single-adapter", "out-of-range", "max-requests"])
+                                  "empty-rows", "all-base", "single-adapter", "out-of-range", "long-rows",
+                                  "max-requests"])
 def test_route_is_bit_exact(case: str) -> None:
     rng = np.random.default_rng(hash(case) % 2**32)
     cu = None
@@ -94,6 +95,10 @@ def test_route_is_bit_exact(case: str) -> None:
         adp, row_len = np.full(33, 7), 3
     elif case == "out-of-range":
         adp = np.array([1, 70, -1, 2, 64, 65])
+    elif case == "long-rows":  # requests longer than a routing workgroup's threads
+        adp = rng.integers(0, 6, 9)
+        cu = np.concatenate([[0], np.cumsum([1, 700, 255, 256, 257, 2049, 0, 513, 3])])
+        pool_rows = 6
     else:  # the largest pass the routing kernel sorts
         adp = rng.integers(0, 1025, _lib.MAX_REQUESTS)
         pool_rows = 1025
@@ -102,8 +107,9 @@ def test_route_is_bit_exact(case: str) -> None:
     assert_route_equal(ws, tokens, want, len(adp))
 
 
-def test_route_flags_unusable_seqlens_and_falls_back_to_identity() -> None:
-    cu = np.array([0, 5, 3, 9])  # decreasing offsets
+@pytest.mark.parametrize("cu", [[0, 5, 3, 9], [0, 1500, 700, 3000]])  # decreasing offsets; few and many tokens
+def test_route_flags_unusable_seqlens_and_falls_back_to_identity(cu: list) -> None:
+    cu = np.array(cu)
     ws, tokens = run_route(np.array([1, 2, 3]), 4, None, cu)
     assert int(ws.status.item()) == _lib.ROUTE_BAD_SEQLENS
     assert np.array_equal(ws.tok_perm[:tokens].cpu().numpy(), np.arange(tokens))
