@@ -7,11 +7,11 @@
  * returns MLORA_OK or a negative status before launching anything. No C++ exception crosses this boundary.
  * A narrow product (at most 256 tokens, few per adapter segment: decode) is two launches on the caller's stream, the
  * first factor then the base product with the second factor fused, plus a third that adds the float32 ranges when
- * the input dimension is split. A split product of short segments (more tokens) is two launches: the base ranges
- * together with the first factor, then the epilogue. A split product forced onto long segments (MLORA_FORCE_BASE_SPLIT) creates,
- * on its first use on a device, one second stream (default priority) and two events for that device, kept until
- * the process ends: its base launch runs there beside the first factor's launch, joined back to the caller's stream
- * by event waits (which a graph capture of the caller's stream records).
+ * the input dimension is split. A split product (more tokens, few per segment) is three: the first factor, the base
+ * ranges, then the epilogue. Every launch of every entry point goes to the stream passed in; the library keeps no
+ * streams, events or device buffers of its own, so calls from several host threads on several streams are safe as
+ * long as they do not share route, workspace, partials or output buffers (calls that share them race, as any two
+ * kernels writing one buffer do).
  *
  * Reference interfaces replaced (paths in the reference checkout, runtime/python/src/jeff_runtime/engine/):
  *   mlora_route        per-token adapter lookup adp[t // row_len]          fast_path.py:167,189; int4_kernels.py:72,113
@@ -20,12 +20,17 @@
  *   mlora_shrink       the LoRA first factor QP = x A^T (_lora_mid_kernel) fast_path.py:159-177
  *   mlora_int4_base_expand  the base tiles + LoRA output epilogue          int4_kernels.py:44-64,105-129
  *   mlora_dequant      dequantize / bf16(q * s) of the kernel layout       int4.py:203-208,258-262
+ *   mlora_int4_plan    int4_tiles (the tile and kernel choice of a shape)   int4_tiles.py:57-71
  *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
  *   mlora_int4_partials_bytes  Workspace.P sizing (split partial products)  int4_kernels.py:150-166
  *   mlora_readout_logits  readout_logits (per-adapter readout)          batched_kernels.py:492-504,522-536
  *   mlora_option_softmax  option_softmax (mask, temperature, softmax)     batched_kernels.py:507-519,539-553
  *   mlora_add_rms      add_rms / rms (residual add + RMSNorm)              fast_path.py:80-100,295-298
  *   mlora_silu_mul     silu_mul (SiLU of the gate half times the up half)  fast_path.py:141-156
+ *   mlora_capture_id   no counterpart: the reference's kernels read adp themselves in every product
+ *                      (fast_path.py:167,189), so it needs no separate routing launch to share between them; the
+ *                      Python Workspace uses this to decide whether a route launched earlier in the same graph
+ *                      capture can be shared (jeff_amd/fast_path.py Workspace.routed)
  */
 #ifndef JEFF_MLORA_H
 #define JEFF_MLORA_H
@@ -127,6 +132,10 @@ typedef struct {
 
 int mlora_abi_version(void);
 
+/* *id = the HIP capture sequence id of `stream` while it is capturing a graph, else 0. MLORA_ELAUNCH when HIP
+ * cannot say (e.g. the legacy stream queried during another stream's global-mode capture). */
+int mlora_capture_id(void* stream, uint64_t* id);
+
 /* Bytes of device workspace a product over `tokens` tokens of a group with `rank_cap` stacked ranks needs. */
 size_t mlora_workspace_bytes(int64_t tokens, int32_t rank_cap);
 
@@ -134,6 +143,16 @@ size_t mlora_workspace_bytes(int64_t tokens, int32_t rank_cap);
  * is NULL, rows of row_len tokens each (tokens = requests * row_len). One launch. */
 int mlora_route(const int32_t* adp, const int32_t* cu_seqlens, int32_t row_len, const mlora_route_t* route,
                 int32_t pool_rows, void* stream);
+
+/* The kernels mlora_int4_linear runs, without running them (host only, no GPU needed): for a pass of `tokens` tokens
+ * in `requests` request rows over a pool of pool_rows rows, through a group of k inputs, `columns` kernel columns,
+ * `out` outputs and rank_cap stacked ranks, with these flags. *base: 0 the GEMV (at most 8 tokens), 1 the MFMA tile
+ * kernel with the second factor fused, 2 the split product, 3 the narrow product; *shrink: 0 the segment form, 1
+ * the MFMA form of the first factor; *ranges: input ranges of a split or narrow product (1 otherwise; the narrow
+ * count depends on the current device's CU count, 256 without a device). MLORA_EUNSUPPORTED as mlora_int4_linear
+ * would return it for forced flags that cannot run. */
+int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int32_t requests, int32_t pool_rows,
+                    int32_t rank_cap, int32_t flags, int32_t* base, int32_t* shrink, int32_t* ranges);
 
 /* The dequantised weights bf16((c - z) s) of `w` as bf16 (out, k), row-major. */
 int mlora_dequant(const mlora_int4_t* w, uint16_t* out, void* stream);

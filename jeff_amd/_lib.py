@@ -36,9 +36,10 @@ def force_ranges(s: int) -> int:
     return s << 8
 
 
-EXPORTS = ("mlora_abi_version", "mlora_workspace_bytes", "mlora_int4_partials_bytes", "mlora_route", "mlora_dequant",
-           "mlora_shrink", "mlora_int4_linear", "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits",
-           "mlora_option_softmax", "mlora_add_rms", "mlora_silu_mul")
+EXPORTS = ("mlora_abi_version", "mlora_capture_id", "mlora_workspace_bytes", "mlora_int4_partials_bytes",
+           "mlora_route", "mlora_dequant", "mlora_int4_plan", "mlora_shrink", "mlora_int4_linear",
+           "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits", "mlora_option_softmax", "mlora_add_rms",
+           "mlora_silu_mul")
 
 c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -86,10 +87,15 @@ def lib() -> ctypes.CDLL:
         P = ctypes.POINTER
         h.mlora_abi_version.restype = c_i32
         h.mlora_abi_version.argtypes = []
+        h.mlora_capture_id.restype = c_i32
+        h.mlora_capture_id.argtypes = [c_vp, P(ctypes.c_uint64)]
         h.mlora_workspace_bytes.restype = ctypes.c_size_t
         h.mlora_workspace_bytes.argtypes = [c_i64, c_i32]
         h.mlora_route.restype = c_i32
         h.mlora_route.argtypes = [c_vp, c_vp, c_i32, P(Route), c_i32, c_vp]
+        h.mlora_int4_plan.restype = c_i32
+        h.mlora_int4_plan.argtypes = [c_i32, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, P(c_i32), P(c_i32),
+                                      P(c_i32)]
         h.mlora_dequant.restype = c_i32
         h.mlora_dequant.argtypes = [P(Int4), c_vp, c_vp]
         h.mlora_shrink.restype = c_i32
@@ -119,6 +125,13 @@ def lib() -> ctypes.CDLL:
             raise LibraryMissing(f"{LIBRARY} has ABI version {version}; this package needs {ABI_VERSION} (rebuild)")
         _lib = h
         return h
+
+
+def capture_id(stream: int) -> int:
+    """HIP's capture sequence id of `stream` (a hipStream_t as an int) while it captures a graph, else 0."""
+    cid = ctypes.c_uint64(0)
+    check(lib().mlora_capture_id(stream, ctypes.byref(cid)), "mlora_capture_id")
+    return int(cid.value)
 
 
 def check(rc: int, what: str) -> None:

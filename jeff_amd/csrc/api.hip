@@ -2,7 +2,6 @@
 // Every check runs on the host, before any launch; nothing here allocates, synchronises or reads device memory, so
 // the entry points can be recorded into a HIP graph.
 #include <climits>
-#include <mutex>
 
 #include "mlora_common.h"
 
@@ -54,6 +53,11 @@ int check_rows(const void* p, int64_t stride, int32_t width) {
   if (p == nullptr || stride < width) return MLORA_EINVAL;
   if (!aligned16(p) || stride % 8) return MLORA_EALIGN;
   return MLORA_OK;
+}
+
+// The first factors (tokens x rank_cap bf16) are addressed with 32-bit buffer offsets.
+int check_first_factors(const mlora_route_t* r, const mlora_lora_t* L) {
+  return r->tokens * (int64_t)L->rank_cap * 2 >= ((int64_t)1 << 31) ? MLORA_EOVERFLOW : MLORA_OK;
 }
 
 // Long segments on average (prefill): at least 16 tokens per adapter segment.
@@ -154,30 +158,6 @@ size_t split_bytes(const mlora_int4_t* w, int64_t tokens) {
   return ((size_t)split_ranges(w, tokens) * (size_t)tokens * (size_t)w->columns * 4 + 255) & ~(size_t)255;
 }
 
-// A second stream and two events per device, made on the first split product: the split product's base launch runs
-// on it beside the first factor's launch (they only read x), and the epilogue launch waits for both. Default
-// priority; the fork and join are ordinary event waits, so a graph capture of the caller's stream records them.
-struct Aux {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-  bool ok = false;
-};
-constexpr int kMaxDevices = 64;
-Aux g_aux[kMaxDevices];
-std::once_flag g_aux_once[kMaxDevices];
-
-const Aux* aux_stream() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::call_once(g_aux_once[dev], [dev] {
-    Aux& x = g_aux[dev];
-    x.ok = hipStreamCreateWithFlags(&x.stream, hipStreamNonBlocking) == hipSuccess &&
-           hipEventCreateWithFlags(&x.fork, hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&x.join, hipEventDisableTiming) == hipSuccess;
-  });
-  return g_aux[dev].ok ? &g_aux[dev] : nullptr;
-}
-
 // The base product (and the LoRA second factor) once mid holds the first factors.
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
@@ -207,6 +187,15 @@ extern "C" {
 
 int mlora_abi_version(void) { return MLORA_ABI_VERSION; }
 
+int mlora_capture_id(void* stream, uint64_t* id) {
+  if (id == nullptr) return MLORA_EINVAL;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &cid) != hipSuccess) return MLORA_ELAUNCH;
+  *id = status == hipStreamCaptureStatusActive ? (uint64_t)cid : 0;
+  return MLORA_OK;
+}
+
 size_t mlora_workspace_bytes(int64_t tokens, int32_t rank_cap) {
   if (tokens <= 0 || rank_cap <= 0) return 256;
   return ((size_t)tokens * (size_t)rank_cap * 2 + 255) & ~(size_t)255;
@@ -225,6 +214,29 @@ int mlora_route(const int32_t* adp, const int32_t* cu_seqlens, int32_t row_len, 
   return launch_route(adp, cu_seqlens, row_len, *route, pool_rows, static_cast<hipStream_t>(stream));
 }
 
+int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int32_t requests, int32_t pool_rows,
+                    int32_t rank_cap, int32_t flags, int32_t* base, int32_t* shrink, int32_t* ranges) {
+  if (base == nullptr || shrink == nullptr || ranges == nullptr) return MLORA_EINVAL;
+  if (k <= 0 || k % 64 || columns <= 0 || columns % 64 || out <= 0 || out > columns || tokens <= 0 || requests < 0 ||
+      pool_rows < 1 || rank_cap < 0)
+    return MLORA_EINVAL;
+  // descriptors holding only what the rule reads
+  const mlora_int4_t w = {nullptr, nullptr, nullptr, k, columns, out, 64};
+  mlora_lora_t L = {};
+  L.pool_rows = pool_rows;
+  L.rank_cap = rank_cap;
+  mlora_route_t r = {};
+  r.tokens = tokens;
+  r.requests = requests;
+  Base b;
+  const int rc = base_of(&w, &L, &r, k, flags, &b);
+  if (rc) return rc;
+  *base = b == Base::gemv ? 0 : b == Base::fused ? 1 : b == Base::split ? 2 : 3;
+  *shrink = shrink_on_mfma(&r, pool_rows, flags) ? 1 : 0;
+  *ranges = b == Base::narrow ? narrow_ranges(&w, flags) : b == Base::split ? split_ranges(&w, tokens) : 1;
+  return MLORA_OK;
+}
+
 int mlora_dequant(const mlora_int4_t* w, uint16_t* out, void* stream) {
   int rc = check_int4(w);
   if (rc) return rc;
@@ -240,7 +252,7 @@ int mlora_shrink(const mlora_lora_t* lora, const mlora_route_t* route, const uin
   if (lora == nullptr || k <= 0 || k % 64) return MLORA_EINVAL;
   int32_t n_out = 0;
   for (int j = 0; j < lora->n_mats && j < MLORA_MAX_MATS; ++j) n_out += lora->cols[j];
-  if ((rc = check_lora(lora, k, n_out))) return rc;
+  if ((rc = check_lora(lora, k, n_out)) || (rc = check_first_factors(route, lora))) return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, k))) return rc;
   if (mid == nullptr) return MLORA_EINVAL;
@@ -263,7 +275,8 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
                       void* stream) {
   int rc = check_int4(w);
   if (rc) return rc;
-  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
+  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out)) || (rc = check_first_factors(route, lora)))
+    return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, w->k))) return rc;
   if (y == nullptr || y_stride < w->out) return MLORA_EINVAL;
@@ -287,20 +300,12 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
   }
   if (base == Base::split) {
-    // split product of long segments: the base launch on the second stream beside the first factor's, then the
-    // epilogue
-    const Aux* aux = aux_stream();
-    if (aux == nullptr) return MLORA_ELAUNCH;
+    // split product of long segments (forced): the first factor, the base ranges, then the epilogue
     const int32_t ks = split_ranges(w, route->tokens);
     float* part = static_cast<float*>(partials);
-    if (hipEventRecord(aux->fork, s) != hipSuccess || hipStreamWaitEvent(aux->stream, aux->fork, 0) != hipSuccess)
-      return MLORA_ELAUNCH;
-    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks,
-                             aux->stream)))
-      return rc;
-    if (hipEventRecord(aux->join, aux->stream) != hipSuccess) return MLORA_ELAUNCH;
     if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
-    if (hipStreamWaitEvent(s, aux->join, 0) != hipSuccess) return MLORA_ELAUNCH;
+    if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
+      return rc;
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
   }
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
@@ -313,7 +318,8 @@ int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, cons
                            const uint16_t* mid, void* partials, size_t partials_bytes, int32_t flags, void* stream) {
   int rc = check_int4(w);
   if (rc) return rc;
-  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out))) return rc;
+  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out)) || (rc = check_first_factors(route, lora)))
+    return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, w->k))) return rc;
   if (y == nullptr || y_stride < w->out || mid == nullptr || !aligned16(mid)) return MLORA_EINVAL;
@@ -329,7 +335,7 @@ int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const u
   int rc = check_route(route);
   if (rc) return rc;
   if (k <= 0 || k % 64 || n_out <= 0) return MLORA_EINVAL;
-  if ((rc = check_lora(lora, k, n_out))) return rc;
+  if ((rc = check_lora(lora, k, n_out)) || (rc = check_first_factors(route, lora))) return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, k))) return rc;
   if (y == nullptr || y_stride < n_out) return MLORA_EINVAL;

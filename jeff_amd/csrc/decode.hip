@@ -292,10 +292,18 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
         }
         // sB operands of segment s (ranks rc + 16 k16 + 8 (lane >> 5) .. +7): unconditional loads inside the
         // adapter's block (clamped to its last 8 ranks), masked when used
+        // The wave's first 64 segments are held one per lane; empty segments (requests of no tokens) can put more
+        // than 64 segment indices across its 64 rows, and those past the 64th are read from memory (i is uniform).
         auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
-          const int i = min(s, s_hi) - s_lo;
-          const int a = __builtin_amdgcn_readlane(la, i);
-          const int live = __builtin_amdgcn_readlane(llive, i);
+          const int sc = min(s, s_hi), i = sc - s_lo;
+          int a, live;
+          if (i < kWave) {
+            a = __builtin_amdgcn_readlane(la, i);
+            live = __builtin_amdgcn_readlane(llive, i);
+          } else {
+            a = r.seg_adapter[sc];
+            live = a == 0 ? 0 : live_rank(L, a, j);
+          }
           rk = s <= s_hi ? min(live - rc, kDRankChunk) : 0;
           const int sbs = sb_stride(live, capj);  // at least 8: capj > rc >= 0
           const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;

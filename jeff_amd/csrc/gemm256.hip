@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // set to zero. The first two segments' adapters and live ranks of the first matrix were read in the prologue.
   if (lora) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)mid, (short)0, (int)(T * L.rank_cap * 2), 0x00020000);
+        (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
     const int jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
     for (int j = jlo; j <= jhi; ++j) {
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);

@@ -23,7 +23,9 @@ Everything on the GPU runs in the HIP library (jeff_amd/libjeff_mlora.so); there
 from __future__ import annotations
 
 import bisect
-from collections.abc import Mapping, Sequence
+import weakref
+from collections.abc import Callable, Mapping, Sequence
+from dataclasses import dataclass
 
 import torch
 
@@ -155,6 +157,41 @@ class Lin:
         return lora_add(x @ self.W.T, x, self, adp, ws)
 
 
+@dataclass(frozen=True)
+class RouteRecord:
+    """What the last routing launch of a workspace routed: the adp tensor (by identity) and its version, the pass's
+    sizes, the cu_seqlens tensor and version (None for uniform rows), the stream and the graph capture it went to
+    (HIP's capture sequence id, 0 outside a capture)."""
+    adp: Callable[[], torch.Tensor | None]
+    adp_version: int
+    requests: int
+    tokens: int
+    pool_rows: int
+    cu: Callable[[], torch.Tensor | None] | None
+    cu_version: int
+    stream: int
+    capture: int
+
+
+def reusable(last: RouteRecord, adp: torch.Tensor, tokens: int, pool_rows: int, stream: int, capture: int) -> bool:
+    """Whether a product may read the route `last` describes instead of routing again: only inside the graph capture
+    that recorded that routing launch (so every replay runs it first), on the same stream, for the same adp tensor
+    object unchanged since (its version counter; a new tensor at a reused address is another object) and unchanged
+    cu_seqlens. Outside a capture a product always routes again: graph replays of the same workspace are invisible
+    to Python and may have overwritten the route with another pass's since."""
+    if capture == 0 or last.capture != capture or last.stream != stream:
+        return False
+    if last.adp() is not adp or last.adp_version != adp._version or last.requests != adp.numel():
+        return False
+    if last.tokens != tokens or last.pool_rows != pool_rows:
+        return False
+    if last.cu is not None:
+        cu = last.cu()
+        if cu is None or cu._version != last.cu_version:
+            return False
+    return True
+
+
 class Workspace:
     """fast_path.py:261-274: scratch shared by the products of passes of up to `rows` tokens in request rows of
     `row_len` tokens (uniform rows, as the reference's passes), or ragged rows routed with cu_seqlens.
@@ -187,7 +224,7 @@ class Workspace:
         self.seg_adapter = torch.empty(b, **i32)
         self.num_segs = torch.zeros(1, **i32)
         self.status = torch.zeros(1, **i32)
-        self._routed: tuple | None = None
+        self._last: RouteRecord | None = None
         self._route_abi: _lib.Route | None = None
         self._part: torch.Tensor | None = None
 
@@ -204,10 +241,11 @@ class Workspace:
 
     def route(self, adp: torch.Tensor, pool_rows: int, tokens: int | None = None,
               cu_seqlens: torch.Tensor | None = None) -> _lib.Route:
-        """Sort this pass's request rows by adapter index (one launch on the current stream) and keep the result for
-        every product that follows with the same `adp` (and cu_seqlens). Uniform rows: tokens = len(adp) * row_len.
-        Ragged rows: cu_seqlens int32 (requests + 1) on the device and `tokens` (its last value) given by the caller,
-        since reading it would synchronise."""
+        """Sort this pass's request rows by adapter index: one launch on the current stream, every call. Uniform
+        rows: tokens = len(adp) * row_len. Ragged rows: cu_seqlens int32 (requests + 1) on the device and `tokens`
+        (its last value) given by the caller, since reading it would synchronise. The products that follow with the
+        same adp route it again the same way (with these cu_seqlens), or, inside one graph capture, share this
+        launch (routed)."""
         requests = int(adp.numel())
         if adp.dtype != torch.int32 or adp.device.type != "cuda" or not adp.is_contiguous():
             raise ValueError("adp must be a contiguous int32 tensor on the GPU")
@@ -224,28 +262,34 @@ class Workspace:
                 raise ValueError("cu_seqlens must be a contiguous int32 tensor of requests + 1 offsets")
         if tokens > self.rows:
             raise ValueError(f"A pass of {tokens} tokens does not fit a workspace of {self.rows}")
-        key = (adp.data_ptr(), adp._version, requests, tokens, pool_rows)
-        seq = None if cu_seqlens is None else (cu_seqlens.data_ptr(), cu_seqlens._version)
-        if self._routed == (key, seq) and self._route_abi is not None:
-            return self._route_abi
         r = _lib.Route(self.req_order.data_ptr(), self.tok_perm.data_ptr(), self.last_of.data_ptr(),
-                       self.seg_of.data_ptr(), self.seg_start.data_ptr(), self.seg_adapter.data_ptr(), self.num_segs.data_ptr(),
-                       self.status.data_ptr(), tokens, requests, max(min(requests, pool_rows), 1))
+                       self.seg_of.data_ptr(), self.seg_start.data_ptr(), self.seg_adapter.data_ptr(),
+                       self.num_segs.data_ptr(), self.status.data_ptr(), tokens, requests,
+                       max(min(requests, pool_rows), 1))
         h = _lib.lib()
         stream = torch.cuda.current_stream(adp.device).cuda_stream
         _lib.check(h.mlora_route(adp.data_ptr(), 0 if cu_seqlens is None else cu_seqlens.data_ptr(),
                                  0 if cu_seqlens is not None else self.row_len, r, pool_rows, stream), "mlora_route")
-        self._routed = (key, seq)
+        self._last = RouteRecord(weakref.ref(adp), adp._version, requests, tokens, pool_rows,
+                                 None if cu_seqlens is None else weakref.ref(cu_seqlens),
+                                 -1 if cu_seqlens is None else cu_seqlens._version, stream, _lib.capture_id(stream))
         self._route_abi = r
         return r
 
     def routed(self, adp: torch.Tensor, pool_rows: int, tokens: int) -> _lib.Route:
-        """The route of `adp` for a product of `tokens` tokens: the one this workspace made last for the same adp
-        (uniform or ragged), else a new one over uniform rows."""
-        key = (adp.data_ptr(), adp._version, int(adp.numel()), tokens, pool_rows)
-        if self._routed is not None and self._routed[0] == key and self._route_abi is not None:
+        """The route a product of `tokens` tokens over `adp` reads. Inside a graph capture, the route launched
+        earlier in the same capture for this very adp tensor (unchanged since, same stream) is shared: the graph
+        replays that launch before this product. Otherwise the route is launched again, with the cu_seqlens of the
+        last ws.route of this adp when there was one (ragged rows), else over uniform rows of row_len."""
+        last = self._last
+        stream = torch.cuda.current_stream(adp.device).cuda_stream
+        capture = _lib.capture_id(stream)
+        if last is not None and reusable(last, adp, tokens, pool_rows, stream, capture):
             return self._route_abi
-        return self.route(adp, pool_rows, tokens=tokens)
+        cu = None
+        if last is not None and last.adp() is adp and last.cu is not None:
+            cu = last.cu()
+        return self.route(adp, pool_rows, tokens=tokens, cu_seqlens=cu)
 
     def check(self) -> None:
         """Raise ValueError if the last routing met an adapter index out of range or unusable cu_seqlens (reads the
@@ -351,13 +395,9 @@ class AdapterPool:
         return self.adapter_index[adapter]
 
 
-def attach_int4(lins: Sequence[Lin], packed: Sequence[KernelInt4]) -> int:
-    """fast_path.py:352-363: give every Lin its INT4 weights in the kernel layout; returns the packed bytes."""
-    total = 0
-    for lin, p in zip(lins, packed, strict=True):
-        if p.out != lin.out or p.k != lin.k:
-            raise ValueError(f"{', '.join(lin.names)}: INT4 weights of {p.out} x {p.k}, the group is {lin.out} x "
-                             f"{lin.k}")
-        lin.int4 = p
-        total += p.nbytes()
-    return total
+def attach_int4(lins: Sequence[Lin], quantization) -> int:
+    """fast_path.py:352-363: give every Lin of an INT4 base its INT4 weights in the kernel layout from the folder
+    `quantization` names (jeff_amd.int4_file.Quantization: its int4.safetensors, checked against the record's
+    sha256 and, where the Lin has bfloat16 weights W, against W bit for bit); returns the packed bytes."""
+    from jeff_amd.int4_file import attach_int4 as attach
+    return attach(lins, quantization)

@@ -181,15 +181,13 @@ def unpack_kernel_asym(packed: KernelInt4) -> tuple[torch.Tensor, torch.Tensor, 
 
 def pack_group(stored: Mapping[str, tuple[torch.Tensor, torch.Tensor]], names: Sequence[str],
                dequantised: torch.Tensor) -> KernelInt4:
-    """engine/int4.py:265-277: matrices `names` (stored {name: (qweight uint8 (out, in/2), scales)}) stacked along
-    the output in the kernel layout, after checking that `dequantised` is bf16(q * s) of them bit for bit."""
-    device = dequantised.device
-    q = torch.cat([unpack_int4(stored[name][0].to(device)) for name in names])
-    scales = torch.cat([stored[name][1].to(device) for name in names])
-    group = q.shape[1] // scales.shape[1]
-    if dequantised.dtype != torch.bfloat16 or not torch.equal(dequantize(q, scales, group), dequantised):
-        raise Int4Error(f"The bfloat16 weights of {', '.join(names)} are not bf16(q * s) of their integers and scales")
-    return pack_kernel(q, scales, group)
+    """engine/int4.py:265-277: the kernel layout of the fused group `names` from the folder's stored matrices
+    ({name: (qweight uint8 (out, in/2), scales bf16 (out, in/G))}, as read_int4_file gives them), packed on the
+    device of `dequantised`, the group's bfloat16 weights; those must be bf16(q * s) of the same integers and scales
+    bit for bit (Int4Error naming the group otherwise). The packing itself is int4_file.pack_stored_group's."""
+    from jeff_amd.int4_file import StoredInt4, pack_stored_group
+    return pack_stored_group({name: StoredInt4(*stored[name]) for name in names}, names, dequantised.device,
+                             dequantised)
 
 
 def dequantize_kernel(packed: KernelInt4) -> torch.Tensor:

@@ -20,6 +20,7 @@ import tempfile
 from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
 from pathlib import Path
+from typing import Any
 
 import torch
 from safetensors.torch import load_file, save_file
@@ -175,12 +176,42 @@ def pack_stored_group(stored: Mapping[str, StoredInt4], names: Sequence[str], de
     if dequantised is not None:
         want = torch.cat([dequantize_stored(m) for m in ms])
         if dequantised.dtype != torch.bfloat16 or not torch.equal(want, dequantised.to(device)):
-            raise Int4Error(f"The bfloat16 weights of {', '.join(names)} are not bf16((c - z) s) of their integers and "
+            form = "bf16((c - z) s)" if ms[0].zeros is not None else "bf16(q * s)"
+            raise Int4Error(f"The bfloat16 weights of {', '.join(names)} are not {form} of their integers and "
                             f"scales in {INT4_FILE}")
     scales = torch.cat([m.scales for m in ms])
     if ms[0].zeros is None:
         return pack_kernel(torch.cat([unpack_int4(m.qweight) for m in ms]), scales, group)
     return pack_kernel_asym(torch.cat([_codes(m) for m in ms]), scales, torch.cat([m.zeros for m in ms]), group)
+
+
+@dataclass(frozen=True)
+class Quantization:
+    """The checked "quantization" object of an INT4 base folder with its record (engine/int4.py:55-63). The path
+    reads `folder` (where int4.safetensors lies) and record["int4_sha256"] (the file's digest); the other fields are
+    kept for the reference's interface."""
+    format: str
+    format_id: str
+    method: str
+    source_hashes: dict[str, str]
+    record: dict[str, Any]
+    folder: Path
+
+
+def attach_int4(lins: Sequence, quantization: Quantization) -> int:
+    """fast_path.py:352-363: give every fused group (Lin) its matrices' integers and scales from the folder's
+    int4.safetensors, in the kernel layout, on the device of its bfloat16 weights W (pack_stored_group, which checks
+    that W is bf16(q * s) of them bit for bit), or on the current GPU for a group that has only INT4 weights. Every
+    INT4 matrix must be in exactly one Lin (read_int4_file refuses a missing or an extra one). Returns the packed
+    bytes."""
+    matrices = {name: (size, lin.k) for lin in lins for name, size in zip(lin.names, lin.sizes, strict=True)}
+    stored = read_int4_file(Path(quantization.folder) / INT4_FILE, quantization.record["int4_sha256"], matrices)
+    total = 0
+    for lin in lins:
+        w = getattr(lin, "W", None)
+        lin.int4 = pack_stored_group(stored, lin.names, w.device if w is not None else "cuda", w)
+        total += lin.int4.nbytes()
+    return total
 
 
 def attach_int4_file(lins: Sequence, path: Path, int4_sha256: str | None, device: torch.device | str = "cuda",

@@ -1,28 +1,26 @@
-"""Which HIP kernels run an INT4 product of a given shape (kept apart from the library so the rule can be checked
-without a GPU). The reference chooses Triton tiles here (engine/int4_tiles.py:57-71); the MI355X kernels pick a
-kernel family instead, and the tiles inside each family are fixed for gfx950.
+"""Which HIP kernels run an INT4 product of a given shape. The reference chooses Triton tiles here
+(engine/int4_tiles.py:57-71); the MI355X library picks a kernel family instead, with the tiles inside each family
+fixed for gfx950. The rule lives in the library alone (api.hip); int4_tiles asks it through mlora_int4_plan, a host-only
+call that needs no GPU, so the kernel a benchmark names is the one the product runs.
 
-- base: "gemv" (at most GEMV_MAX_TOKENS tokens: one pass over the weights, every token dotted with each dequantised
-  word), "mfma" (32x32x16 bf16 MFMA tiles, the LoRA second factor fused into the epilogue), "narrow" (few tokens per
-  adapter segment and at most NARROW_MAX_TOKENS tokens: one row tile of every token by 64 columns, the second factor
-  fused, the input dimension split into float32 ranges only when the columns are too few for the CUs) or "split"
-  (few tokens per segment, more tokens: MFMA tiles over ranges of the input dimension into float32 partials, then
-  one epilogue workgroup per adapter segment and 256 columns).
+- base: "gemv" (at most 8 tokens: one pass over the weights, every token dotted with each dequantised word), "mfma"
+  (32x32x16 bf16 MFMA tiles, the LoRA second factor fused into the epilogue), "narrow" (few tokens per adapter
+  segment and at most 256 tokens: one row tile of every token by 64 columns, the second factor fused, the input
+  dimension split into float32 ranges only when the columns are too few for the CUs) or "split" (few tokens per
+  segment, more tokens: MFMA tiles over ranges of the input dimension into float32 partials, then one epilogue
+  workgroup per adapter segment and 256 columns).
 - shrink (the LoRA first factor): "segment" when segments are short on average (decode: one workgroup per segment
   and 32 ranks of its adapter's A, the segment's rows as the second MFMA operand) or "mfma" when they are long
-  (prefill: 32 sorted rows per workgroup on MFMA).
-The library makes the same choice itself when no flag forces one (api.hip, shrink_on_mfma)."""
+  (prefill: 32 sorted rows per workgroup on MFMA)."""
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 from jeff_amd import _lib
 
-GEMV_MAX_TOKENS = 8
-NARROW_MAX_TOKENS = 256
-SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT = 16
-BASES = ("gemv", "mfma", "narrow", "split")
+BASES = ("gemv", "mfma", "split", "narrow")  # in the library's numbering (mlora_int4_plan *base)
 SHRINKS = ("segment", "mfma")
 
 
@@ -30,7 +28,7 @@ SHRINKS = ("segment", "mfma")
 class Int4Tiles:
     base: str
     shrink: str
-    ranges: int | None = None  # a narrow product's input ranges (1, 2, 4 or 8); None: the library's choice
+    ranges: int | None = None  # input ranges of a narrow product (1, 2, 4 or 8); None: the library's choice
 
     def flags(self) -> int:
         f = {"gemv": _lib.FORCE_BASE_GEMV, "mfma": _lib.FORCE_BASE_MFMA, "narrow": _lib.FORCE_BASE_NARROW,
@@ -39,16 +37,27 @@ class Int4Tiles:
         return f | (_lib.FORCE_SHRINK_SEGMENT if self.shrink == "segment" else _lib.FORCE_SHRINK_MFMA)
 
 
-def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = None,
-               pool_rows: int | None = None) -> Int4Tiles:
-    """The kernels for `tokens` tokens in `requests` request rows through a group of `inputs` inputs and `columns`
-    kernel columns; ValueError for a shape the kernels cannot run."""
+def int4_plan(columns: int, inputs: int, tokens: int, requests: int | None = None, pool_rows: int | None = None,
+              rank_cap: int = 0, out: int | None = None, flags: int = 0) -> tuple[str, str, int]:
+    """(base kernel, first-factor kernel, input ranges) the library runs for this shape; ValueError for a shape the
+    kernels cannot run."""
+    requests = tokens if requests is None else requests
+    pool_rows = requests + 1 if pool_rows is None else pool_rows
     if columns <= 0 or columns % 64 or inputs <= 0 or inputs % 64 or tokens <= 0:
         raise ValueError(f"The INT4 kernels need columns and inputs that are positive multiples of 64 and at least one "
                          f"token; got {columns} columns, {inputs} inputs, {tokens} tokens")
-    requests = tokens if requests is None else requests
-    segs = max(1, min(requests, pool_rows if pool_rows is not None else requests))
-    long_segments = tokens >= SHRINK_MFMA_MIN_TOKENS_PER_SEGMENT * segs
-    base = ("gemv" if tokens <= GEMV_MAX_TOKENS else "mfma" if long_segments
-            else "narrow" if tokens <= NARROW_MAX_TOKENS else "split")
-    return Int4Tiles(base, "mfma" if long_segments else "segment")
+    base, shrink, ranges = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    rc = _lib.lib().mlora_int4_plan(inputs, columns, columns if out is None else out, tokens, requests, pool_rows,
+                                    rank_cap, flags, ctypes.byref(base), ctypes.byref(shrink), ctypes.byref(ranges))
+    if rc != _lib.OK:
+        raise ValueError(f"no INT4 kernel runs {tokens} tokens through {inputs} -> {columns} with flags {flags}: "
+                         f"{_lib.ERRORS.get(rc, rc)}")
+    return BASES[base.value], SHRINKS[shrink.value], ranges.value
+
+
+def int4_tiles(columns: int, inputs: int, tokens: int, requests: int | None = None,
+               pool_rows: int | None = None) -> Int4Tiles:
+    """The kernels for `tokens` tokens in `requests` request rows through a group of `inputs` inputs and `columns`
+    kernel columns (the library's choice); ValueError for a shape the kernels cannot run."""
+    base, shrink, _ = int4_plan(columns, inputs, tokens, requests, pool_rows)
+    return Int4Tiles(base, shrink)

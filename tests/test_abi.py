@@ -86,3 +86,25 @@ def test_header_stride_helper_matches_the_package(tmp_path: Path) -> None:
                                                                       check=True).stdout.splitlines()]
     assert len(rows) == sum(c + 1 for c in range(0, 129, 8))
     assert all(s == sb_stride(r, c) for r, c, s in rows)
+
+
+def test_first_factor_extent_past_32_bits_is_refused() -> None:
+    """The first factors (tokens x stacked rank, bf16) are addressed with 32-bit buffer offsets: a pass whose first
+    factors reach 2^31 bytes is refused with MLORA_EOVERFLOW before any launch, one token fewer is not."""
+    h = _lib.lib()
+    mats = (_lib.c_i64 * _lib.MAX_MATS)(64 * 64, *([0] * (_lib.MAX_MATS - 1)))
+    caps = (_lib.c_i32 * _lib.MAX_MATS)(64, *([0] * (_lib.MAX_MATS - 1)))
+    cols = (_lib.c_i32 * _lib.MAX_MATS)(64, *([0] * (_lib.MAX_MATS - 1)))
+    lora = _lib.Lora(16, 16, 2 * 64 * 64, 0, mats, 1, 2, 1, 64, caps, cols)
+    w = _lib.Int4(16, 16, None, 64, 64, 64, 64)
+    for tokens, want in ((1 << 24, _lib.EOVERFLOW), ((1 << 24) - 1, _lib.EINVAL)):
+        r = _lib.Route(16, 16, 16, 16, 16, 16, 16, 16, tokens, 1, 1)
+        # with y missing, a pass that fits stops at the y check (EINVAL); none of these calls launches anything
+        assert h.mlora_int4_linear(ctypes.byref(w), ctypes.byref(lora), ctypes.byref(r), 16, 64, None, 64, None, 16,
+                                   1 << 40, None, 0, 0, None) == want
+        assert h.mlora_lora_add(ctypes.byref(lora), ctypes.byref(r), 16, 64, 64, None, 64, 64, 16, 1 << 40, 0,
+                                None) == want
+    r = _lib.Route(16, 16, 16, 16, 16, 16, 16, 16, 1 << 24, 1, 1)
+    assert h.mlora_shrink(ctypes.byref(lora), ctypes.byref(r), 16, 64, 64, 16, 0, None) == _lib.EOVERFLOW
+    assert h.mlora_int4_base_expand(ctypes.byref(w), ctypes.byref(lora), ctypes.byref(r), 16, 64, 16, 64, None, 16,
+                                    None, 0, 0, None) == _lib.EOVERFLOW

@@ -308,6 +308,37 @@ def test_narrow_products(name: str, ranges) -> None:
     assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
 
 
+@pytest.mark.parametrize("tiles", [None, Int4Tiles("narrow", "segment", 1), Int4Tiles("narrow", "segment", 2),
+                                   Int4Tiles("split", "segment"), Int4Tiles("mfma", "segment")])
+def test_more_segments_than_a_wave_has_lanes(tiles) -> None:
+    """Requests of no tokens still make adapter segments (empty ones). 200 requests, each with its own adapter, in
+    shuffled order; the odd adapters' requests have one token and the even ones' none, so in sorted order every 64
+    rows span 127 segment indices, more than a wave holds one per lane."""
+    n = 200
+    ranks = {a: [(8, 16, 24, 32)[a % 4], (16, 8)[a % 2]] for a in range(1, n + 1)}
+    case = make_case([96, 64], 256, 128, True, ranks, [32, 16], 17)
+    lin = case.lin
+    rng = np.random.default_rng(4)
+    ids = rng.permutation(np.arange(1, n + 1)).astype(np.int32)
+    lengths = (ids % 2).astype(np.int64)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    tokens = int(cu[-1])
+    adp = torch.tensor(ids, device="cuda")
+    cu_d = torch.tensor(cu, device="cuda")
+    x = torch.randn(tokens, lin.k, device="cuda").to(DT)
+    ws = Workspace(tokens, 1, max_rank=lin.rank, max_requests=n)
+    ws.route(adp, lin.pool.shape[0], tokens=tokens, cu_seqlens=cu_d)
+    last = torch.empty(n, lin.out, dtype=DT, device="cuda")
+    got = int4_product(lin, x, ws, adp, tiles=tiles, last_out=last)
+    ws.check()
+    assert int(ws.num_segs.item()) == n
+    ends = np.flatnonzero(lengths)
+    assert torch.equal(last[torch.as_tensor(ends, device="cuda")], got[torch.as_tensor(cu[1:][ends] - 1,
+                                                                                    device="cuda").long()])
+    r = judge(lin, case.w, x, token_ids(adp, lin.pool.shape[0], cu=cu_d), got)
+    assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
+
+
 @pytest.mark.parametrize("tiles", [None, Int4Tiles("mfma", "segment"), Int4Tiles("split", "mfma")])
 def test_ragged_prefill_with_last_token_gather(tiles) -> None:
     """64 requests of U{16..256} tokens, 16 adapters rank 16 on a 1024 -> 3072 g128 asymmetric group; each request's
@@ -373,9 +404,7 @@ def test_two_runs_and_a_graph_replay_give_the_same_bits() -> None:
             int4_product(lin, x, ws, adp, tiles=tiles)
         torch.cuda.current_stream().wait_stream(stream)
         graph = torch.cuda.CUDAGraph()
-        ws._routed = None  # record the routing launch into the graph too
         with torch.cuda.graph(graph):
-            ws.route(adp, lin.pool.shape[0])
             out = int4_product(lin, x, ws, adp, tiles=tiles)
         for _ in range(3):
             graph.replay()

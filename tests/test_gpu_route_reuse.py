@@ -1,0 +1,117 @@
+"""Routing under the reference's own call patterns (needs a gfx950 GPU; marked gpu).
+
+The reference records each pass once and replays it for every batch (engine/batched_path.py:383-398: the inputs
+filled, two warm-up runs of the pass on the recording stream outside the capture, then the capture; each batch then
+copies its rows' adapter ids into the same input tensor and replays, :589-603). The products must route the ids the
+replay finds, not the ones the warm-up saw. Each replay here, with new adapter ids (and, for ragged rows, new
+sequence lengths) copied into the captured tensors, is checked against the oracle on every output row and against
+an eager run of the same inputs bit for bit. Also: passes over temporary adp tensors in a row on one workspace, whose
+storage the allocator may hand from one to the next."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from jeff_amd import _lib
+from jeff_amd.fast_path import DT, Workspace
+from jeff_amd.int4_kernels import int4_product
+from jeff_amd.int4_tiles import Int4Tiles
+from tests.gpu_cases import judge, make_case, token_ids
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu() -> None:
+    assert torch.cuda.is_available(), "the gpu tests need an AMD GPU"
+    _lib.lib()
+
+
+def group_case(seed: int):
+    """Two fused groups reading the same input (a pass's products share its route), 6 adapters of mixed ranks."""
+    ranks = {1: [16, 8], 2: [8, 16], 3: [16, 16], 4: [0, 8], 5: [16, 0], 6: [8, 8]}
+    return [make_case([320, 192], 512, 128, True, ranks, [16, 16], seed),
+            make_case([256], 512, 64, False, {a: [16] for a in range(1, 7)}, [16], seed + 1)]
+
+
+@pytest.mark.parametrize("kind", ["uniform-decode", "uniform-prefill", "ragged-prefill", "ragged-narrow"])
+def test_capture_after_warm_up_then_replay_new_ids(kind: str) -> None:
+    cases = group_case(len(kind))
+    pool_rows = cases[0].lin.pool.shape[0]
+    assert all(c.lin.pool.shape[0] == pool_rows for c in cases)
+    rng = np.random.default_rng(len(kind) * 13)
+    ragged = kind.startswith("ragged")
+    if kind == "uniform-decode":
+        requests, row_len = 64, 1
+    elif kind == "uniform-prefill":
+        requests, row_len = 8, 64
+    else:
+        requests, row_len = 24 if kind == "ragged-prefill" else 96, 1
+    tokens = 640 if kind == "ragged-prefill" else (96 if kind == "ragged-narrow" else requests * row_len)
+
+    def lengths() -> np.ndarray:  # ragged lengths summing to `tokens`, some requests empty
+        cuts = np.sort(rng.choice(np.arange(tokens + 1), requests - 1, replace=True))
+        return np.diff(np.concatenate([[0], cuts, [tokens]]))
+
+    # the pass's input tensors, filled as the reference fills them before recording (batched_path.py:383-388)
+    adp = torch.zeros(requests, dtype=torch.int32, device="cuda")
+    cu = torch.zeros(requests + 1, dtype=torch.int32, device="cuda")
+    cu.copy_(torch.arange(requests + 1, dtype=torch.int32) * (tokens // requests))
+    cu[-1] = tokens
+    x = torch.zeros(tokens, 512, device="cuda", dtype=DT)
+    ws = Workspace(tokens, 1 if ragged else row_len, max_rank=32, max_requests=requests)
+    tiles = Int4Tiles("narrow", "segment") if kind in ("uniform-decode", "ragged-narrow") else None
+
+    def body() -> list[torch.Tensor]:
+        if ragged:
+            ws.route(adp, pool_rows, tokens=tokens, cu_seqlens=cu)
+        return [int4_product(c.lin, x, ws, adp, tiles=tiles) for c in cases]
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):  # warm up outside the capture (batched_path.py:392-395)
+            body()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outs = body()
+
+    for batch in range(3):
+        ids = rng.integers(0, pool_rows, requests).astype(np.int32)
+        adp.copy_(torch.from_numpy(ids))  # the new pass's rows, into the recorded tensors (batched_path.py:601)
+        lens = lengths() if ragged else np.full(requests, row_len)
+        cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        cu.copy_(torch.from_numpy(cu_np))
+        x.copy_(torch.randn(tokens, 512, device="cuda").to(DT))
+        graph.replay()
+        torch.cuda.synchronize()
+        tok = token_ids(adp, pool_rows, cu=cu) if ragged else token_ids(adp, pool_rows, row_len=row_len)
+        eager_ws = Workspace(tokens, 1 if ragged else row_len, max_rank=32, max_requests=requests)
+        for c, got in zip(cases, outs):
+            r = judge(c.lin, c.w, x, tok, got)
+            assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, (kind, batch, r)
+            if ragged:
+                eager_ws.route(adp, pool_rows, tokens=tokens, cu_seqlens=cu)
+            eager = int4_product(c.lin, x, eager_ws, adp, tiles=tiles)
+            assert torch.equal(eager, got), (kind, batch)
+        _ = x.float().sum().item()  # eager work between replays
+
+
+def test_temporary_adp_tensors_in_a_row() -> None:
+    """Each pass builds its adp as a temporary, freed before the next one's is made (the allocator may give the next
+    one the same storage): every product routes the ids it is given."""
+    case = group_case(3)[0]
+    lin = case.lin
+    pool_rows = lin.pool.shape[0]
+    x = torch.randn(256, lin.k, device="cuda").to(DT)
+    ws = Workspace(256, 32, max_rank=lin.rank)
+    rng = np.random.default_rng(9)
+    for _ in range(4):
+        ids = rng.integers(0, pool_rows, 8).astype(np.int32)
+        got = int4_product(lin, x, ws, torch.tensor(ids, device="cuda"))
+        torch.cuda.synchronize()
+        r = judge(lin, case.w, x, np.repeat(ids, 32), got)
+        assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, (ids, r)

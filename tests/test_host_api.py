@@ -157,3 +157,38 @@ def test_product_registry_follows_the_reference_rules() -> None:
         product_candidates(dict.fromkeys(GROUPS, False), [INT4])
     with pytest.raises(ValueError, match="hold no INT4 weights"):
         product_candidates({GROUPS[0]: True, GROUPS[1]: False})
+
+
+def test_a_route_is_shared_only_inside_the_capture_that_launched_it() -> None:
+    """Workspace.routed's rule (reusable): a product reads the last routing launch instead of routing again only
+    inside the same graph capture, on the same stream, for the same adp tensor unchanged since, and the same pass."""
+    import weakref
+
+    from jeff_amd.fast_path import RouteRecord, reusable
+
+    adp = torch.zeros(4, dtype=torch.int32)
+    cu = torch.tensor([0, 1, 3, 3, 9], dtype=torch.int32)
+
+    def record(capture: int, stream: int = 7, with_cu: bool = False) -> RouteRecord:
+        return RouteRecord(weakref.ref(adp), adp._version, 4, 9 if with_cu else 4, 5,
+                           weakref.ref(cu) if with_cu else None, cu._version if with_cu else -1, stream, capture)
+
+    assert reusable(record(11), adp, 4, 5, 7, 11)
+    assert not reusable(record(0), adp, 4, 5, 7, 0)          # eager: always route again
+    assert not reusable(record(0), adp, 4, 5, 7, 11)         # routed before the capture (the warm-up)
+    assert not reusable(record(11), adp, 4, 5, 7, 12)        # another capture
+    assert not reusable(record(11), adp, 4, 5, 8, 11)        # another stream
+    assert not reusable(record(11), adp, 8, 5, 7, 11)        # another token count
+    assert not reusable(record(11), adp, 4, 6, 7, 11)        # another pool
+    other = torch.zeros(4, dtype=torch.int32)
+    assert not reusable(record(11), other, 4, 5, 7, 11)      # an equal tensor that is another object
+    rec = record(11)
+    adp.copy_(torch.tensor([1, 2, 3, 4]))                    # new ids in the same tensor
+    assert not reusable(rec, adp, 4, 5, 7, 11)
+    rec = record(11, with_cu=True)
+    assert reusable(rec, adp, 9, 5, 7, 11)
+    cu[1] = 2                                                # new sequence lengths
+    assert not reusable(rec, adp, 9, 5, 7, 11)
+    rec = record(11)
+    del adp                                                  # the recorded tensor is gone
+    assert not reusable(rec, torch.zeros(4, dtype=torch.int32), 4, 5, 7, 11)

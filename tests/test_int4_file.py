@@ -129,3 +129,62 @@ def test_attach_gives_every_group_its_layout(tmp_path) -> None:
     sha = write_int4_file(tmp_path / "int4.safetensors", mats)
     attach_int4_file([lin], tmp_path / "int4.safetensors", sha, device="cpu")
     assert lin.int4 is not None and lin.int4.out == 192 and lin.int4.k == 128
+
+
+def test_pack_group_from_the_folder_tuples_checks_the_bf16_copy(tmp_path) -> None:
+    """int4.pack_group, the reference's form (engine/int4.py:265-277; its test tests/test_int4.py:282-307): the stored
+    {name: (qweight, scales)} of a fused group stacked along the output, whose integers and scales unpack to the
+    originals, after a bit-for-bit check of the group's bfloat16 copy; a copy one step off or in float32 is refused."""
+    from jeff_amd.int4 import pack_group
+    names = [f"layers.0.linear_attn.{n}" for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a")]
+    mats = {n: sym_matrix(size, 128, 10 + i) for i, (n, size) in enumerate(zip(names, (192, 64, 16, 16)))}
+    sha = write_int4_file(tmp_path / "int4.safetensors", {n: m[2] for n, m in mats.items()})
+    stored = read_int4_file(tmp_path / "int4.safetensors", sha, {n: (m[0].shape[0], 128) for n, m in mats.items()})
+    folder_tuples = {n: (m.qweight, m.scales) for n, m in stored.items()}
+    copy = torch.cat([from_bits(oracle_dequantize((mats[n][0].numpy() + 8).astype(np.uint8), bits(mats[n][1]), None,
+                                                  64)) for n in names])
+    packed = pack_group(folder_tuples, names, copy)
+    assert packed.out == copy.shape[0] == 288 and packed.words.shape[1] % 64 == 0
+    q, scales = unpack_kernel(packed)
+    assert torch.equal(q, torch.cat([mats[n][0] for n in names]))
+    assert torch.equal(scales, torch.cat([mats[n][1] for n in names]))
+    changed = copy.clone()
+    changed[1, 2] += 1
+    with pytest.raises(Int4Error, match=r"The bfloat16 weights of layers.0.linear_attn.in_proj_qkv, "
+                                        r".*in_proj_a are not bf16\(q \* s\) of their integers and scales"):
+        pack_group(folder_tuples, names, changed)
+    with pytest.raises(Int4Error, match=r"are not bf16\(q \* s\)"):
+        pack_group(folder_tuples, names, copy.float())
+
+
+def test_attach_int4_reads_the_folder_the_record_names(tmp_path) -> None:
+    """fast_path.attach_int4(lins, quantization) (fast_path.py:352-363): every Lin gets the layout of its matrices
+    from the folder's int4.safetensors, checked against the record's sha256 and the Lin's bfloat16 W; the packed
+    bytes are returned; a missing matrix or another file is refused."""
+    from jeff_amd.fast_path import Lin, attach_int4
+    from jeff_amd.int4_file import INT4_FILE, Quantization
+    groups = {"qkv": (["l.q_proj", "l.k_proj", "l.v_proj"], [128, 64, 64]), "o": (["l.o_proj"], [128])}
+    mats = {}
+    for i, (names, sizes) in enumerate(groups.values()):
+        for j, (n, size) in enumerate(zip(names, sizes)):
+            mats[n] = sym_matrix(size, 128, 20 + 4 * i + j)
+    sha = write_int4_file(tmp_path / INT4_FILE, {n: m[2] for n, m in mats.items()})
+
+    def copy_of(names):
+        return torch.cat([from_bits(oracle_dequantize((mats[n][0].numpy() + 8).astype(np.uint8), bits(mats[n][1]),
+                                                      None, 64)) for n in names])
+
+    lins = [Lin(names, [copy_of([n]) for n in names]) for names, _ in groups.values()]
+    record = Quantization("int4-g64", "base@v1+int4-g64-rtn." + sha[:8], "rtn", {}, {"int4_sha256": sha}, tmp_path)
+    total = attach_int4(lins, record)
+    assert total == sum(lin.int4.nbytes() for lin in lins)
+    for lin, (names, _) in zip(lins, groups.values()):
+        q, s = unpack_kernel(lin.int4)
+        assert torch.equal(q, torch.cat([mats[n][0] for n in names]))
+        assert torch.equal(s, torch.cat([mats[n][1] for n in names]))
+        assert torch.equal(lin.int4.words, pack_kernel(q, s).words)
+    extra = Lin(["l.gate_proj"], [copy_of(["l.o_proj"])])
+    with pytest.raises(Int4Error, match="lacks 2 tensors"):
+        attach_int4(lins + [extra], record)
+    with pytest.raises(Int4Error, match="has sha256"):
+        attach_int4(lins, Quantization("int4-g64", "x", "rtn", {}, {"int4_sha256": "0" * 64}, tmp_path))
