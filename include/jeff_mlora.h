@@ -49,6 +49,7 @@ extern "C" {
 #define MLORA_READOUT_MAX_DIM 2048  /* hidden size of the decision head's readout */
 #define MLORA_READOUT_MAX_OPTIONS 256  /* answer options per readout */
 #define MLORA_EPILOGUE_MAX_N 8192   /* row length of add_rms */
+#define MLORA_NOALLOC_SCRATCH_BYTES (64u << 20)  /* device scratch of mlora_int4_linear_noalloc, per GPU */
 
 enum {
   MLORA_OK = 0,
@@ -178,6 +179,18 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
                       const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
                       void* workspace, size_t workspace_bytes, void* partials, size_t partials_bytes, int32_t flags,
                       void* stream);
+
+/* mlora_int4_linear with its scratch inside the library: no counterpart in the reference, for callers that cannot
+ * allocate device memory or pass a workspace (code under graph capture that must not allocate, tight serving loops,
+ * harnesses that forbid hipMalloc). The first factors and any float32 partials live in a static device array of
+ * MLORA_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU until the process ends; the call
+ * allocates nothing and returns MLORA_EWORKSPACE before any launch when a pass needs more (mlora_workspace_bytes +
+ * mlora_int4_partials_bytes). Every call on one GPU shares that GPU's array and leaves its contents behind; the
+ * kernels write every scratch byte they read, so nothing needs clearing, but calls that overlap on one GPU (other
+ * streams, other threads) race on it. Same arguments, results and bits as mlora_int4_linear otherwise. */
+int mlora_int4_linear_noalloc(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                              const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                              int32_t flags, void* stream);
 
 /* mlora_int4_linear without its shrink launch: the base product and the LoRA second factor, reading the first
  * factors mid (tokens, rank_cap) that mlora_shrink wrote for the same route and x. */

@@ -16,6 +16,7 @@ MAX_POOL_ROWS = 262144
 READOUT_MAX_DIM = 2048
 READOUT_MAX_OPTIONS = 256
 EPILOGUE_MAX_N = 8192
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 OK, EINVAL, EALIGN, EOVERFLOW, EWORKSPACE, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3, -4, -5, -6
 ERRORS = {EINVAL: "invalid argument (a null pointer, a bad size or shape)",
@@ -38,8 +39,8 @@ def force_ranges(s: int) -> int:
 
 EXPORTS = ("mlora_abi_version", "mlora_capture_id", "mlora_workspace_bytes", "mlora_int4_partials_bytes",
            "mlora_route", "mlora_dequant", "mlora_int4_plan", "mlora_shrink", "mlora_int4_linear",
-           "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits", "mlora_option_softmax", "mlora_add_rms",
-           "mlora_silu_mul")
+           "mlora_int4_linear_noalloc", "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits",
+           "mlora_option_softmax", "mlora_add_rms", "mlora_silu_mul")
 
 c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -103,6 +104,9 @@ def lib() -> ctypes.CDLL:
         h.mlora_int4_linear.restype = c_i32
         h.mlora_int4_linear.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_vp,
                                         ctypes.c_size_t, c_vp, ctypes.c_size_t, c_i32, c_vp]
+        h.mlora_int4_linear_noalloc.restype = c_i32
+        h.mlora_int4_linear_noalloc.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_i32,
+                                                c_vp]
         h.mlora_int4_base_expand.restype = c_i32
         h.mlora_int4_base_expand.argtypes = [P(Int4), P(Lora), P(Route), c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp,
                                              ctypes.c_size_t, c_i32, c_vp]

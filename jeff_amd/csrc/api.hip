@@ -2,8 +2,14 @@
 // Every check runs on the host, before any launch; nothing here allocates, synchronises or reads device memory, so
 // the entry points can be recorded into a HIP graph.
 #include <climits>
+#include <mutex>
 
 #include "mlora_common.h"
+
+// Device scratch of mlora_int4_linear_noalloc: the first factors, then the float32 partials of a split or narrow
+// product. One copy per GPU, held until the process ends. Host code never uses this name as an address: it reads
+// each device's address once with hipGetSymbolAddress (noalloc_scratch) and passes that pointer to the kernels.
+static __device__ __align__(256) uint8_t scratch[MLORA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -180,6 +186,22 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
   return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
 }
 
+// The device address of `scratch` on the current device, looked up once per device (with that device current);
+// nullptr when HIP cannot give it.
+constexpr int kMaxDevices = 64;
+uint8_t* g_scratch[kMaxDevices] = {};
+std::once_flag g_scratch_once[kMaxDevices];
+
+uint8_t* noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch[dev] = static_cast<uint8_t*>(p);
+  });
+  return g_scratch[dev];
+}
+
 }  // namespace
 
 #pragma GCC visibility push(default)
@@ -311,6 +333,25 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
   return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
                   s);
+}
+
+int mlora_int4_linear_noalloc(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
+                              const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
+                              int32_t flags, void* stream) {
+  int rc = check_int4(w);
+  if (rc) return rc;
+  if ((rc = check_route(route)) || (rc = check_lora(lora, w->k, w->out)) || (rc = check_first_factors(route, lora)))
+    return rc;
+  if (route->tokens == 0) return MLORA_OK;
+  Base base;
+  if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
+  const size_t first = mlora_workspace_bytes(route->tokens, lora->rank_cap);  // a multiple of 256
+  const size_t part = mlora_int4_partials_bytes(w, lora, route, flags);
+  if (first > MLORA_NOALLOC_SCRATCH_BYTES || part > MLORA_NOALLOC_SCRATCH_BYTES - first) return MLORA_EWORKSPACE;
+  uint8_t* sp = noalloc_scratch();
+  if (sp == nullptr) return MLORA_ELAUNCH;
+  return mlora_int4_linear(w, lora, route, x, x_stride, y, y_stride, last_out, sp, first, part ? sp + first : nullptr,
+                           part, flags, stream);
 }
 
 int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,

@@ -42,6 +42,8 @@ def test_header_constants_match_the_binding() -> None:
     assert const("MLORA_READOUT_MAX_DIM") == _lib.READOUT_MAX_DIM
     assert const("MLORA_READOUT_MAX_OPTIONS") == _lib.READOUT_MAX_OPTIONS
     assert const("MLORA_EPILOGUE_MAX_N") == _lib.EPILOGUE_MAX_N
+    assert re.search(r"#define MLORA_NOALLOC_SCRATCH_BYTES \(64u << 20\)", text)
+    assert _lib.NOALLOC_SCRATCH_BYTES == 64 << 20
     assert const("MLORA_ROUTE_BAD_ADAPTER") == _lib.ROUTE_BAD_ADAPTER
     assert const("MLORA_ROUTE_BAD_SEQLENS") == _lib.ROUTE_BAD_SEQLENS
     for name, value in (("MLORA_FORCE_BASE_GEMV", _lib.FORCE_BASE_GEMV), ("MLORA_FORCE_BASE_MFMA", _lib.FORCE_BASE_MFMA),
