@@ -32,16 +32,20 @@ int check_lora(const mlora_lora_t* L, int32_t k, int32_t n_out) {
   if (L->n_mats < 1 || L->n_mats > MLORA_MAX_MATS) return MLORA_EUNSUPPORTED;
   if (L->pool_rows < 1 || L->pool_rows > MLORA_MAX_POOL_ROWS || L->ranks_stride < L->n_mats) return MLORA_EINVAL;
   if (!aligned16(L->pool) || L->pool_stride % 8 || L->off_a % 8 || L->off_a < 0) return MLORA_EALIGN;
+  if (L->pool_stride < 0) return MLORA_EINVAL;
   int64_t caps = 0, cols = 0;
   for (int j = 0; j < L->n_mats; ++j) {
     if (L->cap[j] < 0 || L->cols[j] <= 0) return MLORA_EINVAL;
     if (L->cap[j] % 8 || L->off_b[j] % 8 || L->off_b[j] < 0) return MLORA_EALIGN;
-    if (L->off_b[j] + (int64_t)L->cols[j] * L->cap[j] > L->pool_stride) return MLORA_EINVAL;
+    // off_b + cols * cap <= pool_stride, without overflow (cols * cap < 2^62)
+    if (L->off_b[j] > L->pool_stride || (int64_t)L->cols[j] * L->cap[j] > L->pool_stride - L->off_b[j])
+      return MLORA_EINVAL;
     caps += L->cap[j];
     cols += L->cols[j];
   }
   if (caps != L->rank_cap || cols != n_out) return MLORA_EINVAL;
-  if (L->off_a + caps * k > L->pool_stride) return MLORA_EINVAL;
+  // off_a + caps * k <= pool_stride (caps < 2^34, k < 2^31: the product is formed only when it fits)
+  if (L->off_a > L->pool_stride || (caps > 0 && (L->pool_stride - L->off_a) / caps < k)) return MLORA_EINVAL;
   return MLORA_OK;
 }
 
@@ -85,7 +89,8 @@ constexpr int64_t kNarrowMaxTokens = 256;  // the narrow kernel's row tile holds
 // The split product runs the 256 x 256 kernel (32-bit x offsets) and stages first factors of at most
 // MLORA_SPLIT_MAX_RANK stacked ranks.
 bool split_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride) {
-  return L->rank_cap <= MLORA_SPLIT_MAX_RANK && r->tokens * (x_stride > w->k ? x_stride : w->k) < ((int64_t)1 << 31);
+  const int64_t row = x_stride > w->k ? x_stride : w->k;  // tokens < 2^31 (check_route): compare by division
+  return L->rank_cap <= MLORA_SPLIT_MAX_RANK && (r->tokens == 0 || row < ((int64_t)1 << 31) / r->tokens);
 }
 
 // Which base kernels run; EUNSUPPORTED when the flags force one that cannot (forced input ranges: a count of 1, 2,
@@ -242,6 +247,8 @@ int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int
   if (k <= 0 || k % 64 || columns <= 0 || columns % 64 || out <= 0 || out > columns || tokens <= 0 || requests < 0 ||
       pool_rows < 1 || rank_cap < 0)
     return MLORA_EINVAL;
+  if (tokens >= INT_MAX || (int64_t)(k / 8) * columns >= INT_MAX) return MLORA_EOVERFLOW;  // as the products refuse
+  if (requests > MLORA_MAX_REQUESTS) return MLORA_EUNSUPPORTED;
   // descriptors holding only what the rule reads
   const mlora_int4_t w = {nullptr, nullptr, nullptr, k, columns, out, 64};
   mlora_lora_t L = {};
@@ -437,7 +444,7 @@ int mlora_silu_mul(const uint16_t* gu, int64_t gu_stride, uint16_t* y, int64_t y
   if (rows == 0) return MLORA_OK;
   if (gu == nullptr || y == nullptr || gu_stride < 2 * (int64_t)inter || y_stride < inter) return MLORA_EINVAL;
   if (!aligned16(gu) || !aligned16(y) || gu_stride % 8 || y_stride % 8) return MLORA_EALIGN;
-  if (rows * (int64_t)(inter / 8) >= ((int64_t)1 << 31) * 256) return MLORA_EOVERFLOW;
+  if (rows >= (((int64_t)1 << 31) * 256) / (inter / 8)) return MLORA_EOVERFLOW;  // rows * inter / 8 < 2^39
   return launch_silu_mul(gu, gu_stride, y, y_stride, rows, inter, static_cast<hipStream_t>(stream));
 }
 

@@ -87,7 +87,15 @@ def judge(lin: Lin, w: torch.Tensor, x: torch.Tensor, tok_adp: np.ndarray, got: 
     tol = within_tolerance(gc, ref32)
     return {"beyond_bound": int((err > bound).sum()), "worst_over_bound": float((err / bound).max()),
             "outside_tolerance": int((~tol).sum()), "finite": bool(torch.isfinite(gc.float()).all()),
-            "max_abs_err": float(err.max())}
+            "max_abs_err": float(err.max()), "mean_abs_err": float(err.mean())}
+
+
+def mean_abs_error(lin: Lin, w: torch.Tensor, x: torch.Tensor, tok_adp: np.ndarray,
+                   got: torch.Tensor) -> float:
+    """Mean absolute error of `got` against the float64 exact result (the reference's accuracy measure)."""
+    adapters = oracle_adapters(lin, np.unique(tok_adp))
+    exact, _ = exact_and_bound(x.cpu(), w, tok_adp, adapters, lin.sizes, lin.rank)
+    return float((got.cpu().double() - exact).abs().mean())
 
 
 def token_ids(adp: torch.Tensor, pool_rows: int, row_len: int | None = None,

@@ -2,7 +2,9 @@
 
 Each output row depends only on its own input row, the group's weights and its adapter, so checking a sample of rows
 (every request's first and last token among them) with the oracle is an exact check of those rows; the whole output
-is checked for finiteness. The decoder configurations run one of their 28 identical layers (all four fused groups).
+is checked for finiteness. Where the oracle's float64 sums take seconds (every group of decode-28l, gate_up of
+prefill-1layer and of decode-pool-28l: all 4096 rows, about 1000 adapters), every row is checked. The decoder
+configurations run one of their 28 identical layers (all four fused groups).
 - cpu-1024: bf16 base 1024 -> 1024 (torch's GEMM, the reference's "cublas" product) plus lora_add, 256 tokens in 8
   segments of 32, 4 adapters of rank 16;
 - prefill-1layer, decode-28l, prefill-skewed-28l (with the last-token gather), decode-pool-28l: int4_product."""
@@ -54,6 +56,11 @@ def sample_rows(w: workloads.Workload, n_random: int = 48) -> np.ndarray:
     return np.unique(rows)
 
 
+# groups checked on every output row (the oracle's float64 sums take seconds there); the others on sampled rows
+EVERY_ROW = {"prefill-1layer": ("gate_up",), "decode-28l": ("qkv", "o", "gate_up", "down"),
+             "prefill-skewed-28l": (), "decode-pool-28l": ("gate_up",)}
+
+
 @pytest.mark.parametrize("name", ["prefill-1layer", "decode-28l", "prefill-skewed-28l", "decode-pool-28l"])
 def test_config_at_full_shape(name: str) -> None:
     w = workloads.make(name, n_layers=1)
@@ -72,7 +79,7 @@ def test_config_at_full_shape(name: str) -> None:
         if last is not None:
             ends = torch.as_tensor(np.cumsum(w.lengths) - 1, device="cuda")
             assert torch.equal(last, y[ends]), f"{name} {label}: gathered rows differ"
-        r = judge(lin, weights_of(lin.int4), x, tok, y, rows=rows)
+        r = judge(lin, weights_of(lin.int4), x, tok, y, rows=None if label in EVERY_ROW[name] else rows)
         assert r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, f"{name} {label}: {r}"
         del x, y, last
     ws.check()

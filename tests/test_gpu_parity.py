@@ -24,7 +24,7 @@ from jeff_amd.int4_tiles import Int4Tiles
 from oracle import codec
 from oracle.layer import step
 from oracle.routing import route as oracle_route
-from tests.gpu_cases import bf16_bits, judge, make_case, oracle_adapters, token_ids
+from tests.gpu_cases import bf16_bits, judge, make_case, mean_abs_error, oracle_adapters, token_ids
 
 pytestmark = pytest.mark.gpu
 
@@ -241,6 +241,12 @@ def test_reference_pattern_products_are_within_the_bound(tokens: int, row_len: i
     assert got.shape == (tokens, lin.out) and got.dtype == DT
     r = judge(lin, case.w, x, token_ids(adp, lin.pool.shape[0], row_len=row_len), got)
     assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, r
+    # the reference's accuracy gate (tests/test_int4_kernels_cuda.py:196-198): the kernel's mean absolute error
+    # against exact is no larger than the library GEMM's on the dequantised weights plus lora_add
+    lin.W = case.w.cuda()
+    library = lin(x, ws, adp)
+    assert r["mean_abs_err"] <= mean_abs_error(lin, case.w, x, token_ids(adp, lin.pool.shape[0], row_len=row_len),
+                                               library), r
 
 
 @pytest.mark.parametrize("tokens", [1, 3, 8])
@@ -366,7 +372,7 @@ def test_ragged_prefill_with_last_token_gather(tiles) -> None:
 
 def test_lora_add_on_the_library_gemm_is_within_the_uncut_bound() -> None:
     """Lin.__call__ (torch's GEMM on the bf16 W, then lora_add), the reference's "cublas" product, against exact."""
-    from oracle.layer import exact_and_bound, uncut_bound
+    from oracle.layer import exact_and_bound, reference_f32, uncut_bound, within_tolerance
     case = reference_pattern_case(4, 64, False)
     lin = case.lin
     lin.W = case.w.cuda()
@@ -382,6 +388,7 @@ def test_lora_add_on_the_library_gemm_is_within_the_uncut_bound() -> None:
     # does, plus one more step for its reduction order
     allowed = uncut_bound(x.cpu(), case.w, exact, bound) + step(exact.abs())
     assert int(((got.double() - exact).abs() > allowed).sum()) == 0
+    assert bool(within_tolerance(got, reference_f32(x.cpu(), case.w, tok, adapters, lin.sizes)).all())
     again = lin(x, ws, adp)
     assert torch.equal(again.cpu(), got)
 

@@ -115,3 +115,64 @@ def test_temporary_adp_tensors_in_a_row() -> None:
         torch.cuda.synchronize()
         r = judge(lin, case.w, x, np.repeat(ids, 32), got)
         assert r["finite"] and r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, (ids, r)
+
+
+class PoolOps:
+    """Every PyTorch operation, seen from Python, that touches the storage of the adapter pool or its live-rank table
+    (the reference's PoolWrites, tests/test_fast_path_cuda.py:138-166)."""
+
+    def __init__(self, pool) -> None:
+        self.storages = {t.untyped_storage().data_ptr() for t in (pool.lora_pool, pool.ranks)}
+        self.seen: list[str] = []
+
+    def __enter__(self) -> "PoolOps":
+        from torch.utils._python_dispatch import TorchDispatchMode
+
+        outer = self
+
+        class Mode(TorchDispatchMode):
+            def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+                leaves = torch.utils._pytree.tree_leaves((args, kwargs or {}))
+                if any(isinstance(t, torch.Tensor) and t.untyped_storage().data_ptr() in outer.storages
+                       for t in leaves):
+                    outer.seen.append(str(func))
+                return func(*args, **(kwargs or {}))
+
+        self.mode = Mode()
+        self.mode.__enter__()
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.mode.__exit__(*exc)
+
+
+def test_switching_adapter_touches_the_pool_with_no_pytorch_operation() -> None:
+    """As the reference's test_switching_adapter_copies_no_weights (tests/test_fast_path_cuda.py:169-186): adding an
+    adapter writes the pool (the spy sees it), while passes that switch adapter on every call, eagerly or as replays of
+    a recorded pass, read it in place: no PyTorch operation touches the pool or its rank table."""
+    ranks = {1: [16, 8], 2: [8, 16], 3: [16, 16], 4: [0, 8], 5: [16, 0], 6: [8, 8]}
+    case = make_case([320, 192], 512, 128, True, ranks, [16, 16], 7, max_adapters=8)
+    lin, pool = case.lin, case.pool
+    x = torch.randn(64, lin.k, device="cuda").to(DT)
+    ws = Workspace(64, 16, max_rank=lin.rank)
+    adp = torch.zeros(4, dtype=torch.int32, device="cuda")
+    g = torch.Generator().manual_seed(2)
+    with PoolOps(pool) as adding:
+        pool.add_adapter("late", {lin.names[0]: ((torch.randn(16, lin.k, generator=g) / 32).to(DT).cuda(),
+                                                 (torch.randn(lin.sizes[0], 16, generator=g) * 0.02).to(DT).cuda())})
+    assert any("copy_" in op for op in adding.seen), adding.seen  # the spy does see writes to the pool
+    int4_product(lin, x, ws, adp)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = int4_product(lin, x, ws, adp)
+    late = pool.index("late")
+    with PoolOps(pool) as switching:
+        for ids in ([1, 2, 3, 4], [late, 0, 6, late], [5, 5, 0, 2]):
+            adp.copy_(torch.tensor(ids, dtype=torch.int32))
+            graph.replay()
+            eager = int4_product(lin, x, ws, adp)
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+    assert switching.seen == [], switching.seen

@@ -76,3 +76,26 @@ def test_planted_mistakes_are_caught_by_the_bound() -> None:
     assert fails(bad_adapters=swapped)
     assert fails(bad_tok=np.where(tok == 1, 2, tok))
     assert fails(bad_w=w.flip(1))
+
+
+def test_planted_mistakes_are_caught_by_the_uncut_bound() -> None:
+    """The uncut bound (a base rounded to bfloat16 before the LoRA update, as lora_add and the "model" precision
+    round) admits the correct two-rounding restatement but not the same restatement with a plausible mistake: the
+    LoRA term dropped or applied twice, A's rank rows reversed, another adapter's update, transposed weights."""
+    x, w, tok, adapters, cols, r = small_case(3)
+    exact, bound = exact_and_bound(x, w, tok, adapters, cols, r * 2)
+    allowed = uncut_bound(x, w, exact, bound)
+    assert ((layer_model(x, w, tok, adapters, cols).double() - exact).abs() <= allowed).all()
+
+    def fails(bad_adapters=None, bad_tok=None, bad_w=None):
+        got = layer_model(x, bad_w if bad_w is not None else w, bad_tok if bad_tok is not None else tok,
+                          bad_adapters if bad_adapters is not None else adapters, cols)
+        return bool(((got.double() - exact).abs() > allowed).any())
+
+    assert fails(bad_adapters={a: [None] * len(cols) for a in adapters})
+    assert fails(bad_adapters={a: [None if u is None else (u[0], (u[1].float() * 2).to(torch.bfloat16))
+                                   for u in ups] for a, ups in adapters.items()})
+    assert fails(bad_adapters={a: [None if u is None else (u[0].flip(0), u[1]) for u in ups]
+                               for a, ups in adapters.items()})
+    assert fails(bad_tok=np.where(tok == 1, 2, tok))
+    assert fails(bad_w=w.flip(1))
