@@ -73,6 +73,12 @@ enum {
 #define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
 #define MLORA_FORCE_BASE_NARROW 32  /* narrow product (at most 256 tokens): every token in one row tile of 64 columns */
 #define MLORA_FORCE_RANGES(s) ((s) << 8)  /* a narrow product over s = 1, 2, 4 or 8 input ranges (s dividing k / 64) */
+/* Epilogue flag: the group is a gate_up pair (matrix 0 gate, matrix 1 up, out / 2 columns each, out a multiple of
+ * 256); y (and last_out) receive silu(gate) * up, out / 2 columns per row, each element
+ * bf16(bf16(g / (1 + exp(-g))) * u) of the product's rounded gate and up outputs, the bits mlora_silu_mul gives on
+ * the unfused product. Products with this flag never take the GEMV kernel; the split product needs capacities in
+ * {0, 8, 16, 32, 64}; mlora_lora_add refuses it. */
+#define MLORA_EPILOGUE_SILU_MUL 64
 
 /* INT4 weights in the kernel layout (reference int4.py:215-230, plus zero points and g128):
  * words  int32 (k/8, columns): word i of column c holds inputs 8i..8i+7, input 8i+j in bits 4j..4j+3 (the code c);

@@ -95,8 +95,14 @@ bool split_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_
 
 // Which base kernels run; EUNSUPPORTED when the flags force one that cannot (forced input ranges: a count of 1, 2,
 // 4 or 8 dividing the 64-input steps, for a narrow product only).
+// The gated epilogue (MLORA_EPILOGUE_SILU_MUL): 0 when off, else the width of each half (gate, up).
+int32_t gated_width(const mlora_int4_t* w, int32_t flags) {
+  return (flags & MLORA_EPILOGUE_SILU_MUL) ? w->out / 2 : 0;
+}
+
 int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
             Base* out) {
+  const bool gated = (flags & MLORA_EPILOGUE_SILU_MUL) != 0;
   const int32_t fs = (flags >> 8) & 0xF;
   if (fs != 0 && (!(fs == 1 || fs == 2 || fs == 4 || fs == 8) || (w->k / 64) % fs)) return MLORA_EUNSUPPORTED;
   if (flags & MLORA_FORCE_BASE_GEMV) {
@@ -110,14 +116,25 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
     *out = Base::narrow;
   } else if (flags & MLORA_FORCE_BASE_MFMA) {
     *out = Base::fused;
-  } else if (r->tokens <= 8) {
+  } else if (r->tokens <= 8 && !gated) {  // (the GEMV kernel has no gated epilogue: few tokens take the tiles)
     *out = Base::gemv;
   } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
     *out = Base::fused;
   } else {
     *out = r->tokens <= kNarrowMaxTokens ? Base::narrow : Base::split;
   }
-  return fs != 0 && *out != Base::narrow ? MLORA_EUNSUPPORTED : MLORA_OK;
+  if (fs != 0 && *out != Base::narrow) return MLORA_EUNSUPPORTED;
+  if (gated) {
+    // gate and up of equal width, a multiple of 128 (the tiles pair 128 gate columns with the same up columns);
+    // the 256 x 256 kernel for the fused product (32-bit x offsets), the register form of the split epilogue
+    const int64_t inter = w->out / 2;
+    if (*out == Base::gemv || L->n_mats != 2 || w->out % 256 || L->cols[0] != inter || L->cols[1] != inter)
+      return MLORA_EUNSUPPORTED;
+    const int64_t row = x_stride > w->k ? x_stride : w->k;
+    if (*out == Base::fused && r->tokens > 0 && row >= ((int64_t)1 << 31) / r->tokens) return MLORA_EUNSUPPORTED;
+    if (*out == Base::split && !finish_registers(*L)) return MLORA_EUNSUPPORTED;
+  }
+  return MLORA_OK;
 }
 
 // CUs of the current device (256 when it cannot be asked, e.g. on a host without a GPU).
@@ -173,13 +190,16 @@ size_t split_bytes(const mlora_int4_t* w, int64_t tokens) {
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
              void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
+  const int32_t inter = gated_width(w, flags);
   if (base == Base::narrow) {
     const int32_t ks = narrow_ranges(w, flags);
     const size_t need = dec_partials_bytes(*w, ks);
     if (need > 0 && (partials == nullptr || !aligned16(partials) || partials_bytes < need)) return MLORA_EWORKSPACE;
     return launch_dec(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, static_cast<float*>(partials), ks,
-                      s);
+                      s, inter);
   }
+  if (base == Base::fused && inter > 0)
+    return launch_base256(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, nullptr, 1, s, inter);
   if (base != Base::split)
     return launch_base(w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, base == Base::gemv, s);
   if (partials == nullptr || !aligned16(partials) || partials_bytes < split_bytes(w, r->tokens))
@@ -188,7 +208,7 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
   float* part = static_cast<float*>(partials);
   int rc = launch_base256(*w, *L, *r, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s);
   if (rc) return rc;
-  return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
+  return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s, inter);
 }
 
 // The device address of `scratch` on the current device, looked up once per device (with that device current);
@@ -254,6 +274,11 @@ int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int
   mlora_lora_t L = {};
   L.pool_rows = pool_rows;
   L.rank_cap = rank_cap;
+  if (flags & MLORA_EPILOGUE_SILU_MUL) {  // a gate_up group: two halves of out / 2, capacities of the register form
+    L.n_mats = 2;
+    L.cols[0] = L.cols[1] = out / 2;
+    L.cap[0] = L.cap[1] = 8;
+  }
   mlora_route_t r = {};
   r.tokens = tokens;
   r.requests = requests;
@@ -308,7 +333,7 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, w->k))) return rc;
-  if (y == nullptr || y_stride < w->out) return MLORA_EINVAL;
+  if (y == nullptr || y_stride < (gated_width(w, flags) ? w->out / 2 : w->out)) return MLORA_EINVAL;
   if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
   if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
   Base base;
@@ -326,7 +351,8 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, false, s))) return rc;
     if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
       return rc;
-    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
+    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s,
+                         gated_width(w, flags));
   }
   if (base == Base::split) {
     // split product of long segments (forced): the first factor, the base ranges, then the epilogue
@@ -335,7 +361,8 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
     if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
       return rc;
-    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s);
+    return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s,
+                         gated_width(w, flags));
   }
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
   return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
@@ -370,7 +397,8 @@ int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, cons
     return rc;
   if (route->tokens == 0) return MLORA_OK;
   if ((rc = check_rows(x, x_stride, w->k))) return rc;
-  if (y == nullptr || y_stride < w->out || mid == nullptr || !aligned16(mid)) return MLORA_EINVAL;
+  if (y == nullptr || y_stride < (gated_width(w, flags) ? w->out / 2 : w->out) || mid == nullptr || !aligned16(mid))
+    return MLORA_EINVAL;
   Base base;
   if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
   return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
@@ -389,7 +417,7 @@ int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const u
   if (y == nullptr || y_stride < n_out) return MLORA_EINVAL;
   if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
   if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
-  if (flags & MLORA_FORCE_BASE_SPLIT) return MLORA_EUNSUPPORTED;  // no base product to split
+  if (flags & (MLORA_FORCE_BASE_SPLIT | MLORA_EPILOGUE_SILU_MUL)) return MLORA_EUNSUPPORTED;  // y is updated in place
   const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
   if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -51,12 +51,16 @@ __device__ __forceinline__ int64_t part_index(int ks, int n_tiles, int nt, int w
   return ((((int64_t)ks * n_tiles + nt) * 8 + wave) * kDMB * 4 + mb * 4 + g) * 64 + lane;
 }
 
+// GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none
+// of it
+template <bool GATED>
 __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                         const uint16_t* __restrict__ x, int64_t x_stride,
                                                         uint16_t* __restrict__ y, int64_t y_stride,
                                                         uint16_t* __restrict__ last_out, int32_t n_out,
                                                         const uint16_t* __restrict__ mid, int32_t n_tiles,
-                                                        int32_t vec, float4* __restrict__ part, int32_t ksplit) {
+                                                        int32_t vec, float4* __restrict__ part, int32_t ksplit,
+                                                        int32_t inter) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
   const int cg = wave % kDCG, rg = wave / kDCG;
@@ -104,7 +108,8 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   // column's raw scale and zero point, and dequantises it once for the whole workgroup into the step's LDS buffer, at
   // 16-byte chunk t, where the MFMA operand of (column, inputs) reads it; columns past the layout read column 0 and
   // get zero weights (scale 0)
-  const int wcol = n0 + (tid & (kDCols - 1));
+  // gated (inter > 0): the tile's first 32 columns are gate columns 32 nt .. +31, its last 32 the same up columns
+  const int wcol = GATED ? ((tid & 32) ? inter : 0) + nt * 32 + (tid & 31) : n0 + (tid & (kDCols - 1));
   const bool colok = wcol < w.columns;
   const uint32_t gcol = colok ? wcol : 0;
   const uint32_t woff = (gcol + (uint32_t)(tid / kDCols) * w.columns) * 4;
@@ -175,7 +180,7 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   // LoRA bookkeeping issued before the K loop so its loads land during it: each lane's row of block mb and
   // that row's segment (-1 past the pass), and the first factors of the wave's rows for the first matrix of its
   // columns (ranks 0..63); the segments' adapters and live ranks follow once the segment range is known.
-  const int cw0 = n0 + cg * 32;  // the wave's first column
+  const int cw0 = GATED ? (cg ? inter : 0) + nt * 32 : n0 + cg * 32;  // the wave's first column
   const int r_end = min(R0 + 32 * kDMB, T);
   const bool lora = L.n_mats > 0 && mid != nullptr && cw0 < n_out && R0 < r_end;
   const int jlo = lora ? matrix_of(L, cw0) : 0;
@@ -368,6 +373,48 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
     return;
   }
+  if constexpr (GATED) {
+    // gated, one range: the up waves leave their rounded outputs in LDS (the x ring is idle after the K loop); each
+    // gate wave pairs them with its own, lane for lane, and writes silu(gate) * up to output columns 32 nt .. +31
+    uint2* ex = reinterpret_cast<uint2*>(d_x0);
+    lds_sync();  // every wave is done reading the x ring
+    if (cg == 1) {
+#pragma unroll
+      for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          ex[((rg * kDMB + mb) * 4 + g) * 64 + lane] = make_uint2(pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]),
+                                                                  pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]));
+    }
+    lds_sync();
+    if (cg == 0) {
+#pragma unroll
+      for (int mb = 0; mb < kDMB; ++mb) {
+        const int row = R0 + mb * 32 + (lane & 31);
+        if (row >= T) continue;
+        const int64_t orig = d_orig[row];
+        const int64_t lq = d_last[row];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 u = ex[((rg * kDMB + mb) * 4 + g) * 64 + lane];
+          const uint32_t lo = silu_mul2(pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]), u.x);
+          const uint32_t hi = silu_mul2(pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]), u.y);
+          const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
+          if (vec) {
+            *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
+            if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
+          } else {
+            const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+            for (int e = 0; e < 4; ++e) {
+              y[orig * y_stride + col + e] = h[e];
+              if (lq >= 0) last_out[lq * inter + col + e] = h[e];
+            }
+          }
+        }
+      }
+    }
+    return;
+  }
   // one range: round once and write four columns per lane and group (rows in their original order)
 #pragma unroll
   for (int mb = 0; mb < kDMB; ++mb) {
@@ -436,6 +483,56 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_kernel(const float4* 
   }
 }
 
+// The same for a gated product: thread f takes float4 f of the gate waves' partial tiles (column group 0 of every row
+// group) and the matching float4 of the up waves' (column group 1), adds each over the ranges in order, rounds both
+// and writes silu(gate) * up to its row's four output columns 32 nt + 8 g + 4 (lane >> 5) .. +3.
+__global__ __launch_bounds__(kDRedThreads) void dec_reduce_gated_kernel(const float4* __restrict__ part,
+                                                                        int32_t ksplit, int32_t n_tiles,
+                                                                        mlora_route_t r, uint16_t* __restrict__ y,
+                                                                        int64_t y_stride,
+                                                                        uint16_t* __restrict__ last_out,
+                                                                        int32_t inter, int32_t vec) {
+  const int64_t per = (int64_t)n_tiles * 8 * kDMB * 4 * 64;  // float4s per range
+  const int64_t f = (int64_t)blockIdx.x * kDRedThreads + threadIdx.x;
+  if (f >= per / 2) return;
+  const int lane = (int)(f & 63);
+  const int64_t q = f >> 6;
+  const int g = (int)(q & 3), mb = (int)((q >> 2) % kDMB);
+  const int64_t t2 = (q >> 2) / kDMB;
+  const int rg = (int)(t2 % kDRG), nt = (int)(t2 / kDRG);
+  const int row = rg * 32 * kDMB + mb * 32 + (lane & 31);
+  const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
+  if (row >= r.tokens) return;
+  const int64_t fg = part_index(0, n_tiles, nt, rg * kDCG, mb, g, lane);
+  const int64_t fu = part_index(0, n_tiles, nt, rg * kDCG + 1, mb, g, lane);
+  float4 gv = part[fg], uv = part[fu];
+  for (int ks = 1; ks < ksplit; ++ks) {
+    const float4 a = part[(int64_t)ks * per + fg], b = part[(int64_t)ks * per + fu];
+    gv.x += a.x;
+    gv.y += a.y;
+    gv.z += a.z;
+    gv.w += a.w;
+    uv.x += b.x;
+    uv.y += b.y;
+    uv.z += b.z;
+    uv.w += b.w;
+  }
+  const uint32_t lo = silu_mul2(pack_bf16x2(gv.x, gv.y), pack_bf16x2(uv.x, uv.y));
+  const uint32_t hi = silu_mul2(pack_bf16x2(gv.z, gv.w), pack_bf16x2(uv.z, uv.w));
+  const int64_t orig = r.tok_perm[row];
+  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
+  if (vec) {
+    *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
+    if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
+  } else {
+    const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+    for (int e = 0; e < 4; ++e) {
+      y[orig * y_stride + col + e] = h[e];
+      if (lq >= 0) last_out[lq * inter + col + e] = h[e];
+    }
+  }
+}
+
 }  // namespace
 
 size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit) {
@@ -445,23 +542,31 @@ size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit) {
 
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
   if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit) return MLORA_EINVAL;
+  if (inter > 0 && (inter % 32 || n_out != 2 * inter)) return MLORA_EINVAL;
   if (ksplit > 1 && part == nullptr) return MLORA_EWORKSPACE;
-  const int n_tiles = w.columns / kDCols;
+  const int n_tiles = inter > 0 ? inter / 32 : w.columns / kDCols;
+  const int out_cols = inter > 0 ? inter : n_out;  // columns of y and last_out
   // 8-byte stores of four columns need 8-byte aligned output rows
   const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
-                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0));
+                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && out_cols % 4 == 0));
   float4* p4 = reinterpret_cast<float4*>(part);
-  hipLaunchKernelGGL(dec_kernel, dim3((unsigned)(n_tiles * ksplit)), dim3(kDThreads), 0, stream, w, L, r, x, x_stride,
-                     y, y_stride, last_out, n_out, mid, n_tiles, (int32_t)vec, p4, ksplit);
+  hipLaunchKernelGGL(inter > 0 ? dec_kernel<true> : dec_kernel<false>, dim3((unsigned)(n_tiles * ksplit)),
+                     dim3(kDThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, n_tiles,
+                     (int32_t)vec, p4, ksplit, inter);
   if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
   if (ksplit > 1) {
     const int64_t per = (int64_t)n_tiles * kDRows * kDCols / 4;
-    hipLaunchKernelGGL(dec_reduce_kernel, dim3((unsigned)((per + kDRedThreads - 1) / kDRedThreads)),
-                       dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, n_out,
-                       (int32_t)vec);
+    if (inter > 0)
+      hipLaunchKernelGGL(dec_reduce_gated_kernel, dim3((unsigned)((per / 2 + kDRedThreads - 1) / kDRedThreads)),
+                         dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, inter,
+                         (int32_t)vec);
+    else
+      hipLaunchKernelGGL(dec_reduce_kernel, dim3((unsigned)((per + kDRedThreads - 1) / kDRedThreads)),
+                         dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, n_out,
+                         (int32_t)vec);
     if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
   }
   return MLORA_OK;

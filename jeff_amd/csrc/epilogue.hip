@@ -73,8 +73,6 @@ __global__ __launch_bounds__(kRmsRows * 64) void add_rms_kernel(const uint16_t* 
   }
 }
 
-__device__ __forceinline__ float silu_bf16(float g) { return bf16_lo(pack_bf16x2(g / (1.0f + __expf(-g)), 0.0f)); }
-
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t gu_stride,
                                                        uint16_t* __restrict__ y, int64_t y_stride, int64_t rows,
                                                        int32_t inter) {
@@ -86,12 +84,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   const uint16_t* gr = gu + row * gu_stride;
   const uint4 gv = *reinterpret_cast<const uint4*>(gr + 8 * c);
   const uint4 uv = *reinterpret_cast<const uint4*>(gr + inter + 8 * c);
-  const uint32_t g4[4] = {gv.x, gv.y, gv.z, gv.w}, u4[4] = {uv.x, uv.y, uv.z, uv.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    o[e] = pack_bf16x2(silu_bf16(bf16_lo(g4[e])) * bf16_lo(u4[e]), silu_bf16(bf16_hi(g4[e])) * bf16_hi(u4[e]));
-  *reinterpret_cast<uint4*>(y + row * y_stride + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+  *reinterpret_cast<uint4*>(y + row * y_stride + 8 * c) = silu_mul8(gv, uv);
 }
 
 }  // namespace

@@ -290,21 +290,169 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlo
   }
 }
 
+// The gated form (the group's matrices 0 and 1 are gate and up, inter columns each): one workgroup per (segment, 128
+// output columns c0 .. c0 + 127); threads 0..127 finish gate columns c0 .. +127 and threads 128..255 the same up
+// columns, each half as finish_columns does with 128 threads (CPC chunks per column, CPC from the larger of the two
+// sB row strides: the half with the smaller stride leaves the extra chunks unread and zero). The gate half then pairs
+// its rounded outputs with the up half's in LDS and writes silu(gate) * up.
+template <int CPC, int MAXS>
+__device__ __forceinline__ void finish_gated_columns(const mlora_lora_t& L, const mlora_route_t& r,
+                                                     const float* __restrict__ part, int32_t ksplit, int32_t ld,
+                                                     const uint16_t* __restrict__ mid, uint16_t* __restrict__ y,
+                                                     int64_t y_stride, uint16_t* __restrict__ last_out, int32_t inter,
+                                                     int64_t sb, int64_t se, int a, int c0, bool vec,
+                                                     float* __restrict__ base_lds, uint16_t* __restrict__ out_lds) {
+  const int tid = threadIdx.x;
+  const int h = tid >> 7, t = tid & 127;  // half (matrix j = h) and thread within it
+  const int ch = t % CPC, cl = t / CPC;
+  const int rk = a != 0 ? live_rank(L, a, h) : 0;
+  const int rho = rank_offset(L, h);
+  const int rc = L.rank_cap;
+  const int sbs = sb_stride(rk, L.cap[h]);
+  const bool chunk_live = 8 * ch < rk;
+  const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[h] + (int64_t)c0 * sbs;
+  const int64_t T = r.tokens;
+  const int oj = h * inter;  // the half's first column in the group's output order
+  uint4 bv[CPC];
+  const int srow = t / 32, scol = 4 * (t % 32);
+  for (int64_t p0 = sb; p0 < se; p0 += kRegRows) {
+    const int rows = (int)min((int64_t)kRegRows, se - p0);
+    const int64_t prow = p0 + min(srow, rows - 1);
+    const int64_t yrow_off = (int64_t)r.tok_perm[prow] * y_stride;
+    const int q = last_out != nullptr ? r.last_of[prow] : -1;
+    float4 pv[MAXS];
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp)
+      pv[sp] = (sp < ksplit && srow < rows)
+                   ? *reinterpret_cast<const float4*>(part + ((int64_t)sp * T + p0 + srow) * ld + oj + c0 + scol)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint4 mv[kRegRows];
+#pragma unroll
+    for (int rr = 0; rr < kRegRows; ++rr)
+      mv[rr] = (chunk_live && rr < rows)
+                   ? keep_first(*reinterpret_cast<const uint4*>(mid + (p0 + rr) * rc + rho + 8 * ch), rk - 8 * ch)
+                   : make_uint4(0, 0, 0, 0);
+    if (p0 == sb) {
+#pragma unroll
+      for (int i = 0; i < CPC; ++i) {
+        const int col = cl + (128 / CPC) * i;
+        bv[i] = chunk_live ? keep_first(*reinterpret_cast<const uint4*>(blk + (int64_t)col * sbs + 8 * ch), rk - 8 * ch)
+                           : make_uint4(0, 0, 0, 0);
+      }
+    }
+    float4 bsum = pv[0];
+#pragma unroll
+    for (int sp = 1; sp < MAXS; ++sp) {
+      bsum.x += pv[sp].x;
+      bsum.y += pv[sp].y;
+      bsum.z += pv[sp].z;
+      bsum.w += pv[sp].w;
+    }
+    __syncthreads();  // the previous pass is done with both LDS tiles
+    *reinterpret_cast<float4*>(&base_lds[srow * kFinThreads + h * 128 + scol]) = bsum;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPC; ++i) {
+      const int col = h * 128 + cl + (128 / CPC) * i;
+#pragma unroll
+      for (int rr = 0; rr < kRegRows; ++rr) {
+        if (rr >= rows) break;
+        const float lora = group_sum<CPC>(dot8(bv[i], mv[rr], 0.0f));
+        if (rr % CPC == ch) out_lds[rr * kFinThreads + col] = f32_to_bf16(base_lds[rr * kFinThreads + col] + lora);
+      }
+    }
+    __syncthreads();
+    if (h == 0 && srow < rows) {
+      const uint2 g = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
+      const uint2 u = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + 128 + scol]);
+      const uint2 v = make_uint2(silu_mul2(g.x, u.x), silu_mul2(g.y, u.y));
+      const int c = c0 + scol;
+      uint16_t* yrow = y + yrow_off;
+      if (vec) {
+        *reinterpret_cast<uint2*>(yrow + c) = v;
+        if (q >= 0) *reinterpret_cast<uint2*>(last_out + (int64_t)q * inter + c) = v;
+      } else {
+        const uint16_t hv[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
+        for (int e = 0; e < 4; ++e) {
+          yrow[c + e] = hv[e];
+          if (q >= 0) last_out[(int64_t)q * inter + c + e] = hv[e];
+        }
+      }
+    }
+  }
+}
+
+template <int MAXS>
+__global__ __launch_bounds__(kFinThreads) void finish_gated_kernel(mlora_lora_t L, mlora_route_t r,
+                                                                  const float* __restrict__ part, int32_t ksplit,
+                                                                  int32_t ld, const uint16_t* __restrict__ mid,
+                                                                  uint16_t* __restrict__ y, int64_t y_stride,
+                                                                  uint16_t* __restrict__ last_out, int32_t inter,
+                                                                  int32_t vec) {
+  __shared__ __attribute__((aligned(16))) float base_lds[kRegRows * kFinThreads];
+  __shared__ __attribute__((aligned(16))) uint16_t out_lds[kRegRows * kFinThreads];
+  const int s = blockIdx.y;
+  if (s >= *r.num_segs) return;
+  const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+  if (se <= sb) return;
+  const int c0 = blockIdx.x * 128;
+  const int a = r.seg_adapter[s];
+  const int sg = sb_stride(a != 0 ? live_rank(L, a, 0) : 0, L.cap[0]);
+  const int su = sb_stride(a != 0 ? live_rank(L, a, 1) : 0, L.cap[1]);
+  switch (max(sg, su)) {  // the larger sB row stride of the two matrices
+    case 64:
+      finish_gated_columns<8, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
+                                    vec != 0, base_lds, out_lds);
+      break;
+    case 32:
+      finish_gated_columns<4, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
+                                    vec != 0, base_lds, out_lds);
+      break;
+    case 16:
+      finish_gated_columns<2, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
+                                    vec != 0, base_lds, out_lds);
+      break;
+    default:
+      finish_gated_columns<1, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
+                                    vec != 0, base_lds, out_lds);
+      break;
+  }
+}
+
 }  // namespace
+
+bool finish_registers(const mlora_lora_t& L) {
+  bool ok = true;
+  for (int j = 0; j < L.n_mats; ++j) {
+    const int c = L.cap[j];
+    ok = ok && (c == 0 || c == 8 || c == 16 || c == 32 || c == 64) && L.cols[j] % 4 == 0;
+  }
+  return ok;
+}
 
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                  hipStream_t stream) {
+                  hipStream_t stream, int32_t inter) {
   if (r.tokens == 0 || n_out == 0 || r.max_segs == 0) return MLORA_OK;
+  if (inter > 0) {
+    if (inter % 128 || L.n_mats != 2 || L.cols[0] != inter || L.cols[1] != inter || !finish_registers(L))
+      return MLORA_EINVAL;
+    const dim3 grid((unsigned)(inter / 128), (unsigned)r.max_segs);
+    const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
+                     (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 8 == 0);
+    if (ksplit == 1)
+      hipLaunchKernelGGL(finish_gated_kernel<1>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
+                         y_stride, last_out, inter, (int32_t)vec);
+    else
+      hipLaunchKernelGGL(finish_gated_kernel<kMaxSplit>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld,
+                         mid, y, y_stride, last_out, inter, (int32_t)vec);
+    return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
+  }
   int blocks = 0;
   // the register form: every cap_j in {0, 8, 16, 32, 64} and every matrix a multiple of four columns (its partial
   // sums are read four columns at a time)
-  bool registers = true;
-  for (int j = 0; j < L.n_mats; ++j) {
-    blocks += (L.cols[j] + kFinThreads - 1) / kFinThreads;
-    const int c = L.cap[j];
-    registers = registers && (c == 0 || c == 8 || c == 16 || c == 32 || c == 64) && L.cols[j] % 4 == 0;
-  }
+  const bool registers = finish_registers(L);
+  for (int j = 0; j < L.n_mats; ++j) blocks += (L.cols[j] + kFinThreads - 1) / kFinThreads;
   const dim3 grid((unsigned)blocks, (unsigned)r.max_segs);
   // 8-byte stores of four columns: 8-byte aligned output rows
   const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&

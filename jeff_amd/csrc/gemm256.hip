@@ -44,15 +44,16 @@ __shared__ __attribute__((aligned(16))) uint16_t g_x3[kTM * kTK];  // the output
 __shared__ int32_t g_orig[kTM];  // the tile's rows: original token index, -1 past the tokens
 __shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it is, else -1
 
-// MB: 32-row blocks of a tile (8: 256 rows; 7: 224 rows, chosen by the host when it takes fewer rounds of tiles)
-template <int MB>
+// MB: 32-row blocks of a tile (8: 256 rows; 7: 224 rows, chosen by the host when it takes fewer rounds of tiles);
+// GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none of it
+template <int MB, bool GATED>
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
                                                                const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec,
                                                                float* __restrict__ part, int32_t ksplit,
-                                                               int32_t base_blocks) {
+                                                               int32_t base_blocks, int32_t inter) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
   // Block b -> (K range ks, row tile mt, column tile nt), column tiles innermost: the blocks that share x rows (one
@@ -64,6 +65,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   constexpr int kRows = 32 * MB;  // the tile's rows (LDS buffers hold 256; rows past kRows are loaded, never used)
   const int64_t p0 = (int64_t)mt * kRows;
   const int n0 = nt * kTN;
+  // The wave's first column: its 32 of the tile's 256; in a gated product (inter > 0: gate columns [0, inter), up
+  // columns [inter, 2 inter)) the tile pairs gate columns 128 nt .. +127 (waves 0..3) with the same up columns
+  // (waves 4..7), and writes silu(gate) * up to output columns 128 nt .. +127.
+  const int wc0 = GATED ? (wave < 4 ? 0 : inter) + nt * 128 + (wave & 3) * 32 : n0 + wave * 32;
 
   // Loads go through buffer resources: the per-lane byte offsets below stay fixed for the whole K loop and the K
   // position is a wave-uniform scalar offset, so no 64-bit addresses are kept in registers. The resources' sizes
@@ -105,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
   // weights: lane l of wave w holds column n0 + 32 w + (l & 31) and, for 16 inputs k16, the word of inputs
   // 16 k16 + 8 (l >> 5) .. +7; columns past the layout read column 0 and get zero weights (scale 0)
-  const int wcol = n0 + wave * 32 + (lane & 31);
+  const int wcol = wc0 + (lane & 31);
   const bool colok = wcol < w.columns;
   const uint32_t gcol = colok ? wcol : 0;
   const uint32_t woff = (gcol + (uint32_t)(lane >> 5) * w.columns) * 4;
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // not count): the tile's first and last adapter segments, the first two segments' adapters and their live ranks of
   // the tile's first matrix.
   const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
-  const int jlo = lora ? matrix_of(L, n0) : 0;
+  const int jlo = lora ? matrix_of(L, GATED ? nt * 128 : n0) : 0;
   int s_lo = 0, s_hi = -1, a_pre[2] = {0, 0}, live_pre[2] = {0, 0};
   if (lora) {
     auto sload = [](const int32_t* q, int64_t i) __attribute__((always_inline)) {
@@ -270,11 +275,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   if (lora) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
-    const int jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
+    const int jhi = matrix_of(L, GATED ? inter + nt * 128 + 127 : min(n0 + kTN, n_out) - 1);
     for (int j = jlo; j <= jhi; ++j) {
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
       // the wave's column inside matrix j (others get zero operands)
-      const int cc = n0 + wave * 32 + (lane & 31);
+      const int cc = wc0 + (lane & 31);
       const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
       const int ccol = (cin ? cc : oj) - oj;
       for (int rc = 0; rc < capj; rc += kRankChunk) {
@@ -369,6 +374,35 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       }
   }
   lds_sync();
+  if constexpr (GATED) {
+    // gated: 16-byte chunk c of a row's gate columns (first buffer of the pair) with the same chunk of its up columns
+    // (second buffer), silu(gate) * up to output columns 128 nt + 8 c .. +7
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f = tid + kThreads * i;
+      const int half = f >> 11, row = (f >> 4) & 127, c = f & 15;
+      const int64_t orig = g_orig[half * 128 + row];
+      if (orig < 0) continue;
+      const int64_t lq = g_last[half * 128 + row];
+      const uint16_t* gb = half == 0 ? g_x0 : g_x2;
+      const uint16_t* ub = half == 0 ? g_x1 : g_x3;
+      const int off = row * 128 + ((c ^ (row & 15)) << 3);
+      const uint4 v = silu_mul8(*reinterpret_cast<const uint4*>(&gb[off]), *reinterpret_cast<const uint4*>(&ub[off]));
+      const int col = nt * 128 + c * 8;
+      if (vec) {
+        *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
+        if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * inter + col) = v;
+      } else {
+        const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
+          y[orig * y_stride + col + e] = h;
+          if (lq >= 0) last_out[lq * inter + col + e] = h;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int f = tid + kThreads * i;
@@ -414,21 +448,20 @@ int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
 
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream) {
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
-  const int n_tiles = (n_out + kTN - 1) / kTN;
+  if (inter > 0 && (part != nullptr || inter % 128 || n_out != 2 * inter)) return MLORA_EINVAL;
+  const int n_tiles = inter > 0 ? inter / 128 : (n_out + kTN - 1) / kTN;
   const int mb = tile_blocks(r.tokens, n_tiles, ksplit);
   const int m_tiles = (int)((r.tokens + 32 * mb - 1) / (32 * mb));
   const int64_t blocks = (int64_t)m_tiles * n_tiles * ksplit;
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
-                   (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);
+                   (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);  // gated: inter % 128 == 0
   const dim3 grid((unsigned)blocks);
-  if (mb == 7)
-    hipLaunchKernelGGL(base_mfma256_kernel<7>, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride,
-                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks);
-  else
-    hipLaunchKernelGGL(base_mfma256_kernel<8>, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride,
-                       last_out, n_out, mid, n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks);
+  auto kernel = inter > 0 ? (mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
+                          : (mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid,
+                     n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks, inter);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

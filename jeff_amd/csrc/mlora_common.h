@@ -67,6 +67,20 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// The gated activation of two packed bf16 pairs (the reference's silu_mul, engine/fast_path.py:141-156): for gate g and
+// up u, bf16(bf16(g / (1 + exp(-g))) u), lo and hi halves independently. Shared by silu_mul_kernel and the products
+// that apply it in their output tiles, so both give the same bits.
+__device__ __forceinline__ float silu_bf16(float g) {
+  const float v = g / (1.0f + __expf(-g));
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v) << 16);
+}
+__device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
+  return pack_bf16x2(silu_bf16(bf16_lo(g2)) * bf16_lo(u2), silu_bf16(bf16_hi(g2)) * bf16_hi(u2));
+}
+__device__ __forceinline__ uint4 silu_mul8(uint4 g, uint4 u) {
+  return make_uint4(silu_mul2(g.x, u.x), silu_mul2(g.y, u.y), silu_mul2(g.z, u.z), silu_mul2(g.w, u.w));
+}
+
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
@@ -155,19 +169,23 @@ int launch_dequant(const mlora_int4_t& w, uint16_t* out, hipStream_t stream);
 int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x, int64_t x_stride, int32_t k,
                   uint16_t* mid, bool mfma, hipStream_t stream);
 // 256 x 256 tiles; with part != nullptr the split mode: ksplit input ranges, float32 sums to part, nothing else.
+// inter > 0: a gated product (the group is gate and up, inter columns each; y and last_out receive silu(gate) * up,
+// inter columns), fused mode only.
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream);
-// The second launch of a split product: partial sums in order + LoRA term, rounded once.
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0);
+// The second launch of a split product: partial sums in order + LoRA term, rounded once (inter > 0: gated, as above;
+// the register form's capacities only, finish_registers).
+bool finish_registers(const mlora_lora_t& L);
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                  hipStream_t stream);
+                  hipStream_t stream, int32_t inter = 0);
 // Narrow product (every token, at most 256, in one row tile of 64 columns): ksplit input ranges; with ksplit > 1
 // part holds dec_partials_bytes(w, ksplit) and a second launch adds the ranges.
 size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit);
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream);
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

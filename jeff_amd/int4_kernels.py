@@ -18,15 +18,33 @@ from jeff_amd.fast_path import DT, Lin, Workspace, _check_input
 from jeff_amd.int4_tiles import Int4Tiles
 
 
+EPILOGUES = (None, "silu_mul")
+
+
+def _epilogue(lin: Lin, epilogue: str | None) -> tuple[int, int]:
+    """(flag bits, output columns) of an epilogue; ValueError for one the group cannot take."""
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"Unknown epilogue {epilogue!r}; expected one of {EPILOGUES}")
+    if epilogue is None:
+        return 0, lin.out
+    if len(lin.sizes) != 2 or lin.sizes[0] != lin.sizes[1] or lin.sizes[0] % 128:
+        raise ValueError(f"{', '.join(lin.names)}: the silu_mul epilogue takes a gate and an up matrix of one width, a "
+                         f"multiple of 128; got widths {lin.sizes}")
+    return _lib.EPILOGUE_SILU_MUL, lin.sizes[0]
+
+
 def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, tiles: Int4Tiles | None = None,
-                 last_out: torch.Tensor | None = None) -> torch.Tensor:
+                 last_out: torch.Tensor | None = None, epilogue: str | None = None) -> torch.Tensor:
     """The fused product of x (M, in) through `lin`'s INT4 weights plus each token's adapter update (the pool row of
     its request row in adp, or the route ws.route made). `tiles` forces the kernel families (tests); `last_out`
-    (requests, lin.out) bf16 also receives each request's last-token output row."""
+    (requests, columns) bf16 also receives each request's last-token output row. epilogue="silu_mul" (a gate_up
+    group: gate then up, one width each): the result is silu_mul of the product, (M, width) (the reference's
+    silu_mul(product(...)), engine/batched_path.py:271, in the product's own output tile, bit for bit)."""
     packed = lin.int4
     if packed is None:
         raise ValueError(f"{', '.join(lin.names)}: no INT4 weights (attach_int4 gives them to an INT4 base's fused "
                          "groups only)")
+    eflag, cols = _epilogue(lin, epilogue)
     _check_input(lin, x, "the INT4 product")
     m = x.shape[0]
     if m >= 2 ** 31 - 1:
@@ -35,13 +53,13 @@ def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, ti
         raise ValueError(f"the GEMV base product runs at most 8 tokens; got {m}")
     if lin.rank > ws.max_rank:
         raise ValueError(f"{', '.join(lin.names)}: stacked rank {lin.rank} exceeds the workspace's {ws.max_rank}")
-    if last_out is not None and (last_out.dtype != DT or last_out.dim() != 2 or last_out.shape[1] != lin.out
+    if last_out is not None and (last_out.dtype != DT or last_out.dim() != 2 or last_out.shape[1] != cols
                                  or not last_out.is_contiguous() or last_out.shape[0] < adp.numel()):
-        raise ValueError(f"last_out must be a contiguous bfloat16 (requests, {lin.out}) tensor")
+        raise ValueError(f"last_out must be a contiguous bfloat16 (requests, {cols}) tensor")
     r = ws.routed(adp, lin.pool.shape[0], m)
-    y = torch.empty(m, lin.out, device=x.device, dtype=DT)
+    y = torch.empty(m, cols, device=x.device, dtype=DT)
     h = _lib.lib()
-    flags = 0 if tiles is None else tiles.flags()
+    flags = (0 if tiles is None else tiles.flags()) | eflag
     w, lora = packed.abi(), lin.lora_abi()
     part, part_bytes = ws.partials(h.mlora_int4_partials_bytes(w, lora, r, flags))
     stream = torch.cuda.current_stream(x.device).cuda_stream
@@ -67,19 +85,21 @@ def shrink(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, mfma: bo
 
 
 def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: torch.Tensor,
-                tiles: Int4Tiles | None = None, last_out: torch.Tensor | None = None) -> torch.Tensor:
+                tiles: Int4Tiles | None = None, last_out: torch.Tensor | None = None,
+                epilogue: str | None = None) -> torch.Tensor:
     """int4_product without its first launch, into a given y: the base product and the LoRA second factor, reading
     the first factors the last shrink (or int4_product) of the same x and adp left in the workspace."""
     packed = lin.int4
     if packed is None:
         raise ValueError(f"{', '.join(lin.names)}: no INT4 weights")
+    eflag, cols = _epilogue(lin, epilogue)
     _check_input(lin, x, "the INT4 product")
     m = x.shape[0]
-    if y.dtype != DT or tuple(y.shape) != (m, lin.out) or y.stride(1) != 1:
-        raise ValueError(f"y must be bfloat16 ({m}, {lin.out}) with contiguous rows")
+    if y.dtype != DT or tuple(y.shape) != (m, cols) or y.stride(1) != 1:
+        raise ValueError(f"y must be bfloat16 ({m}, {cols}) with contiguous rows")
     r = ws.routed(adp, lin.pool.shape[0], m)
     h = _lib.lib()
-    flags = 0 if tiles is None else tiles.flags()
+    flags = (0 if tiles is None else tiles.flags()) | eflag
     w, lora = packed.abi(), lin.lora_abi()
     part, part_bytes = ws.partials(h.mlora_int4_partials_bytes(w, lora, r, flags))
     stream = torch.cuda.current_stream(x.device).cuda_stream

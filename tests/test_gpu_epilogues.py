@@ -122,3 +122,65 @@ def test_epilogues_refuse_bad_arguments() -> None:
         silu_mul(torch.zeros(4, 24, device="cuda", dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="bfloat16"):
         silu_mul(torch.zeros(4, 32, device="cuda"))
+
+
+FUSED_CASES = {  # name: (tokens per request, requests, adapters, gate/up width, inputs, tiles, the kernel chosen)
+    "decode-narrow": (1, 160, 12, 512, 2048, None, "narrow"),
+    "decode-narrow-ranges": (1, 96, 12, 256, 1024, "narrow-4", "narrow"),
+    "decode-few-tokens": (1, 5, 12, 256, 512, "narrow", "narrow"),
+    "decode-split": (1, 600, 48, 256, 1024, None, "split"),
+    "prefill-fused": (64, 24, 12, 384, 1024, None, "mfma"),
+    "prefill-tail": (40, 26, 12, 128, 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED_CASES))
+def test_silu_mul_in_the_product_tile_equals_silu_mul_of_the_product(name: str) -> None:
+    """int4_product(..., epilogue="silu_mul") on a gate_up group (gate then up, one width) against silu_mul of the
+    plain product (the same tiles), bit for bit, for every kernel family that takes it (narrow with and without input
+    ranges, few tokens, split, the 256 x 256 tiles with a partial last tile), with the last-token rows gathered; and
+    against the oracle's silu_mul of the plain product."""
+    from jeff_amd.fast_path import Workspace
+    from jeff_amd.int4_kernels import int4_product
+    from jeff_amd.int4_tiles import Int4Tiles
+    from tests.gpu_cases import make_case
+
+    from jeff_amd import _lib
+    from jeff_amd.int4_tiles import int4_plan
+
+    row_len, requests, adapters, width, k, forced, kernel = FUSED_CASES[name]
+    print(f"fused silu_mul {name}", flush=True)
+    ranks = {a: [(8, 16, 32)[a % 3], (16, 8, 32)[a % 3]] for a in range(1, adapters + 1)}
+    case = make_case([width, width], k, 128, True, ranks, [32, 32], width + k)
+    lin = case.lin
+    tokens = row_len * requests
+    rng = np.random.default_rng(tokens)
+    adp = torch.tensor(rng.integers(0, adapters + 1, requests).astype(np.int32), device="cuda")
+    x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
+    ws = Workspace(tokens, row_len, max_rank=lin.rank)
+    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-4": Int4Tiles("narrow", "segment", 4),
+             "mfma": Int4Tiles("mfma", "mfma")}[forced]
+    flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_SILU_MUL
+    assert int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)[0] == kernel
+    plain = int4_product(lin, x, ws, adp, tiles=tiles)
+    last = torch.zeros(requests, width, dtype=torch.bfloat16, device="cuda")
+    fused = int4_product(lin, x, ws, adp, tiles=tiles, last_out=last, epilogue="silu_mul")
+    assert fused.shape == (tokens, width)
+    assert torch.equal(fused, silu_mul(plain))
+    assert torch.equal(last, fused[row_len - 1::row_len])
+    y_exact, y_bits, _ = oracle_silu_mul(bits(plain))
+    check_close(fused, y_exact, y_bits, f"fused silu_mul {name}")
+
+
+def test_silu_mul_epilogue_refusals() -> None:
+    from jeff_amd.fast_path import Workspace
+    from jeff_amd.int4_kernels import int4_product
+    from tests.gpu_cases import make_case
+
+    case = make_case([256, 128], 512, 128, True, {1: [8, 8]}, [8, 8], 3)
+    x = torch.randn(8, 512, device="cuda").to(torch.bfloat16)
+    adp = torch.ones(8, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="gate and an up matrix of one width"):
+        int4_product(case.lin, x, Workspace(8, 1, max_rank=16), adp, epilogue="silu_mul")
+    with pytest.raises(ValueError, match="Unknown epilogue"):
+        int4_product(case.lin, x, Workspace(8, 1, max_rank=16), adp, epilogue="gelu")
