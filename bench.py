@@ -3,7 +3,8 @@
 of its dominant kernel, with the CPU restatement of the reference's torch layer timed beside it.
 
 A step is one pass over one batch: route the request rows by adapter, then every fused group of every layer
-(int4_product: LoRA first factor, then the INT4 base product with the second factor fused) and, where the workload
+(int4_product: LoRA first factor, then the INT4 base product with the second factor fused; the decoder's gate_up
+group writes SiLU(gate) * up from its output tile, the activation the down product reads) and, where the workload
 gathers each request's last-token output (prefill-skewed-28l), the decision head on it. The step is recorded once
 as a HIP graph and replayed. Inputs (weights, adapter pool, activations) are resident in HBM before timing.
 
@@ -32,6 +33,7 @@ PEAK_BF16 = 2.5e15     # flop/s, MI355X dense bf16 MFMA
 HEADLINE = "prefill-skewed-28l"
 ALSO = ("decode-28l", "decode-pool-28l", "prefill-1layer")
 DOMINANT = "gate_up"   # the largest group of every workload: its layer-0 product is the dominant kernel
+EPILOGUE = {"gate_up": "silu_mul"}  # SiLU(gate) * up in the gate_up product's output tile (decoder workloads)
 BOX_THREADS = 16       # the host threads one GPU's share of the machine offers
 REFERENCE_THREADS = 8  # the reference's default torch thread count (engine/model.py:166-170)
 CPU_SAMPLE_TOKENS = 16384  # tokens of the CPU baseline's sample (the pass's first requests up to at least this)
@@ -122,7 +124,8 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
     from jeff_amd.epilogues import add_rms, silu_mul
     from jeff_amd.fast_path import DT, Workspace
     from jeff_amd.int4_kernels import base_expand, int4_product, shrink
-    from jeff_amd.int4_tiles import int4_tiles
+    from jeff_amd import _lib
+    from jeff_amd.int4_tiles import int4_plan
     from jeff_amd.readout import readout_rows
 
     dev = torch.device("cuda:0")
@@ -150,7 +153,8 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
             for label, lin in layer.items():
                 x = xs[(li if per_layer_acts else 0, label)]
                 gather = last if (last is not None and li == len(w.layers) - 1 and label == "down") else None
-                keep.append(int4_product(lin, x, ws, w.adp, last_out=gather))
+                epi = EPILOGUE.get(label) if w.gated else None
+                keep.append(int4_product(lin, x, ws, w.adp, last_out=gather, epilogue=epi))
         if w.readout is not None:  # the decision head on each request's last-token output
             keep.append(readout_rows(last, w.readout["readout_pool"], w.readout["temp_pool"], w.adp,
                                      w.readout["counts"]))
@@ -187,17 +191,20 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
     # and subtracted.
     lin = w.layers[0][DOMINANT]
     x = xs[(0, DOMINANT)]
-    y = torch.empty(w.tokens, lin.out, dtype=DT, device=dev)
+    gated = w.gated and DOMINANT in EPILOGUE
+    epi = EPILOGUE.get(DOMINANT) if gated else None
+    out_cols = lin.out // 2 if gated else lin.out
+    y = torch.empty(w.tokens, out_cols, dtype=DT, device=dev)
     ws.route(w.adp, pool_rows, tokens=w.tokens, cu_seqlens=w.cu_seqlens)
     shrink(lin, x, ws, w.adp)
-    base_expand(lin, x, ws, w.adp, y)
+    base_expand(lin, x, ws, w.adp, y, epilogue=epi)
     torch.cuda.synchronize()
     kflops = 2.0 * w.tokens * lin.k * lin.out
     tok = workloads.token_ids(w)
     mean_rank = float(sum(w.adapter_ranks.get(int(a), 0) for a in tok)) / max(len(tok), 1)
     kflops += 2.0 * w.tokens * mean_rank * lin.out
     present = sorted({int(a) for a in tok} - {0})
-    kbytes = float(lin.int4.nbytes()) + 2.0 * w.tokens * (lin.k + lin.out)
+    kbytes = float(lin.int4.nbytes()) + 2.0 * w.tokens * (lin.k + out_cols)
     kbytes += sum(2.0 * min(w.adapter_ranks[a], c) * n for a in present for n, c in zip(lin.sizes, lin.caps))
     reps = kernel_reps or max(5, min(200, int(2e12 / max(kflops, 1.0))))
     stream = torch.cuda.current_stream()
@@ -206,7 +213,7 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
         def fn() -> None:
             ws.route(w.adp, pool_rows, tokens=w.tokens, cu_seqlens=w.cu_seqlens)
             for _ in range(k):
-                base_expand(lin, x, ws, w.adp, y)
+                base_expand(lin, x, ws, w.adp, y, epilogue=epi)
         return fn
 
     kgraph = capture(route_then(reps), 1)
@@ -222,16 +229,20 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
         achieved = kbytes / (kms / 1e3)
         roof = {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                 "frac": achieved / PEAK_HBM, "traffic": measured_traffic(name)}
-    tiles = int4_tiles(lin.int4.columns, lin.k, w.tokens, w.requests, pool_rows)
-    kernel = {"mfma": "base_mfma256_kernel (INT4 base + fused LoRA expand)" if w.tokens >= 1024 else
+    base, _, ranges = int4_plan(lin.int4.columns, lin.k, w.tokens, w.requests, pool_rows, lin.rank, lin.out,
+                                _lib.EPILOGUE_SILU_MUL if gated else 0)
+    fin = " + silu(gate) * up" if gated else ""
+    kernel = {"mfma": f"base_mfma256_kernel (INT4 base + fused LoRA expand{fin})" if w.tokens >= 1024 or gated else
               "base_mfma_kernel<true> (INT4 base + fused LoRA expand)",
-              "split": "base_mfma256_kernel, split mode + finish_kernel (INT4 base + LoRA expand, 2 launches)",
-              "narrow": "dec_kernel (INT4 base + fused LoRA expand; dec_reduce_kernel adds split input ranges)",
-              "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[tiles.base]
+              "split": f"base_mfma256_kernel, split mode ({ranges} input ranges) + "
+                       f"{'finish_gated_kernel' if gated else 'finish_kernel'} (INT4 base + LoRA expand{fin})",
+              "narrow": f"dec_kernel (INT4 base + fused LoRA expand{fin}; {ranges} input ranges"
+                        + (", added by dec_reduce_kernel)" if ranges > 1 else ")"),
+              "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[base]
     roof.update({"kernel": kernel, "group": f"layer0.{DOMINANT}", "launch_ms": kms, "reps": reps,
                  "route_ms_subtracted": route_ms, "flops_per_launch": kflops, "bytes_per_launch": kbytes})
     step_flops = workloads.flops_per_token(w) * w.tokens
-    step_bytes = workloads.hbm_bytes(w)
+    step_bytes = workloads.hbm_bytes(w, gated=tuple(EPILOGUE) if w.gated else ())
     step_roof = {"mfma_frac": step_flops / (ms_per_step / 1e3) / PEAK_BF16,
                  "hbm_frac": step_bytes / (ms_per_step / 1e3) / PEAK_HBM,
                  "flops": step_flops, "bytes": step_bytes}
@@ -241,6 +252,21 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
               "adapters": len(w.adapter_ranks), "ranks": sorted(set(w.adapter_ranks.values())),
               "group_size": 128, "zero_points": True, "roofline": roof, "step_roofline": step_roof}
     note(f"{name}: dominant kernel {kms:.4f} ms, {roof['frac']:.3f} of the {roof['bound']} roofline")
+
+    if gated:
+        # SiLU(gate) * up in the product's output tile against the plain product followed by the separate silu_mul
+        # launch: the whole gate_up product (first factor included) each way, timed alone as above
+        g_reps = max(3, min(100, reps))
+        plain = capture(lambda: silu_mul(int4_product(lin, x, ws, w.adp)), g_reps)
+        fused = capture(lambda: int4_product(lin, x, ws, w.adp, epilogue="silu_mul"), g_reps)
+        plain_ms, fused_ms = replay_ms(plain, stream, g_reps), replay_ms(fused, stream, g_reps)
+        del plain, fused
+        inter = lin.out // 2
+        result["fused_silu_mul"] = {"group": f"layer0.{DOMINANT}", "plain_product_and_silu_mul_ms": plain_ms,
+                                    "fused_product_ms": fused_ms,
+                                    "hbm_bytes_saved": 2.0 * w.tokens * inter * 4,
+                                    "note": "the plain product writes 2 inter columns, silu_mul reads them and writes "
+                                            "inter; the fused product writes inter columns once"}
 
     if w.readout is not None:  # the decision head alone: its two launches, timed as the dominant kernel is
         r = w.readout

@@ -74,7 +74,8 @@ enum {
 #define MLORA_FORCE_BASE_NARROW 32  /* narrow product (at most 256 tokens): every token in one row tile of 64 columns */
 #define MLORA_FORCE_RANGES(s) ((s) << 8)  /* a narrow product over s = 1, 2, 4 or 8 input ranges (s dividing k / 64) */
 /* Epilogue flag: the group is a gate_up pair (matrix 0 gate, matrix 1 up, out / 2 columns each, out a multiple of
- * 256); y (and last_out) receive silu(gate) * up, out / 2 columns per row, each element
+ * 256, one rank capacity of at most 64 for both); y (and last_out) receive silu(gate) * up, out / 2 columns per row,
+ * each element
  * bf16(bf16(g / (1 + exp(-g))) * u) of the product's rounded gate and up outputs, the bits mlora_silu_mul gives on
  * the unfused product. Products with this flag never take the GEMV kernel; the split product needs capacities in
  * {0, 8, 16, 32, 64}; mlora_lora_add refuses it. */

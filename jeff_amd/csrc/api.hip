@@ -128,7 +128,8 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
     // gate and up of equal width, a multiple of 128 (the tiles pair 128 gate columns with the same up columns);
     // the 256 x 256 kernel for the fused product (32-bit x offsets), the register form of the split epilogue
     const int64_t inter = w->out / 2;
-    if (*out == Base::gemv || L->n_mats != 2 || w->out % 256 || L->cols[0] != inter || L->cols[1] != inter)
+    if (*out == Base::gemv || L->n_mats != 2 || w->out % 256 || L->cols[0] != inter || L->cols[1] != inter ||
+        L->cap[0] != L->cap[1] || L->cap[0] > 64)
       return MLORA_EUNSUPPORTED;
     const int64_t row = x_stride > w->k ? x_stride : w->k;
     if (*out == Base::fused && r->tokens > 0 && row >= ((int64_t)1 << 31) / r->tokens) return MLORA_EUNSUPPORTED;

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // the tile's first matrix.
   const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
   const int jlo = lora ? matrix_of(L, GATED ? nt * 128 : n0) : 0;
-  int s_lo = 0, s_hi = -1, a_pre[2] = {0, 0}, live_pre[2] = {0, 0};
+  int s_lo = 0, s_hi = -1, a_pre[2] = {0, 0}, live_pre[2] = {0, 0}, live_up[2] = {0, 0};
   if (lora) {
     auto sload = [](const int32_t* q, int64_t i) __attribute__((always_inline)) {
       return ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)q)[i];
@@ -213,6 +213,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     for (int u = 0; u < 2; ++u) {
       const int rk = a_pre[u] == 0 ? 0 : sload(L.ranks, (int64_t)a_pre[u] * L.ranks_stride + jlo);
       live_pre[u] = min(max(rk, 0), L.cap[jlo]);
+      if constexpr (GATED) {  // and of the up matrix, which waves 4..7 add
+        const int ru = a_pre[u] == 0 ? 0 : sload(L.ranks, (int64_t)a_pre[u] * L.ranks_stride + 1);
+        live_up[u] = min(max(ru, 0), L.cap[1]);
+      }
     }
   }
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
@@ -272,7 +276,89 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // straight from memory as MFMA operands (the next segment's issued before the current one's products), and the
   // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
   // set to zero. The first two segments' adapters and live ranks of the first matrix were read in the prologue.
-  if (lora) {
+  if constexpr (GATED) {
+    // Gated: gate and up have one capacity c <= 64 (the host checks it), so their stacked ranks [0, 2c) are staged at
+    // once ([0, 64) in the first buffer, [64, 128) in the second) and each wave adds only its own matrix's term
+    // (waves 0..3 gate, waves 4..7 up).
+    if (lora) {
+      const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
+      const bool two = L.rank_cap > kRankChunk;
+      const int j = wave < 4 ? 0 : 1, capj = L.cap[j];
+      lds_sync();  // every wave is done reading the x ring
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 1 && !two) break;
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+          const int row = (8 * i + wave) * 8 + (lane >> 3);
+          const uint32_t off =
+              (uint32_t)(((p0 + row) * L.rank_cap + h * kRankChunk + (swz_slot(row, lane & 7) << 3)) * 2);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)((h ? g_x1 : g_x0) + (8 * i + wave) * 8 * kTK),
+                                                   16, off, 0, 0, 0);
+        }
+      }
+      // the lane's staged rows: row mb * 32 + (lane & 31) of the buffer holding its matrix's ranks, whose 16-byte
+      // chunk c sits in slot c ^ key; the matrix's ranks start at chunk o8 (16 k16 + 8 (lane >> 5) then in chunk
+      // o8 + 2 k16 + (lane >> 5) <= 7 for every k16 below the capacity)
+      const uint4* mrow = reinterpret_cast<const uint4*>(j == 1 && two ? g_x1 : g_x0) + (lane & 31) * 8;
+      const int key = ((lane & 31) >> 1) & 7;
+      const int cb = (j == 1 && !two ? capj / 8 : 0) + (lane >> 5);
+      const int ccol = wcol - (j ? inter : 0);        // the lane's column inside its matrix
+      // sB operands of segment s for ranks 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
+      auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+        int a, live;
+        if (s - s_lo < 2) {  // read ahead in the prologue
+          a = a_pre[s - s_lo];
+          live = j == 0 ? live_pre[s - s_lo] : live_up[s - s_lo];
+        } else {
+          a = r.seg_adapter[s];
+          live = a == 0 ? 0 : live_rank(L, a, j);
+        }
+        rk = live;
+        const int sbs = sb_stride(live, capj);
+        const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+#pragma unroll
+        for (int k16 = 0; k16 < 4; ++k16) {
+          const int q = min(16 * k16 + 8 * (lane >> 5), sbs - 8);
+          bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+        }
+      };
+      auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+        if (rk <= 0) return;
+        const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
+#pragma unroll
+        for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int64_t r0 = p0 + mb * 32;
+          if (r0 >= se || r0 + 32 <= sb) continue;
+          const int64_t row = r0 + (lane & 31);
+          const bool rin = row >= sb && row < se;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            if (16 * k16 >= rk) break;
+            uint4 av = mrow[mb * 256 + ((cb + 2 * k16) ^ key)];
+            av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+            acc[mb] = mfma32(bv[k16], av, acc[mb]);
+          }
+        }
+      };
+      uint4 b0[4], b1[4];
+      int rk0, rk1;
+      load_b(s_lo, b0, rk0);
+      MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
+      lds_sync();
+      for (int s = s_lo; s <= s_hi; s += 2) {
+        load_b(min(s + 1, s_hi), b1, rk1);
+        apply(s, b0, rk0);
+        if (s + 1 > s_hi) break;
+        load_b(min(s + 2, s_hi), b0, rk0);
+        apply(s + 1, b1, rk1);
+      }
+    }
+  }
+  if (lora && !GATED) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
     const int jhi = matrix_of(L, GATED ? inter + nt * 128 + 127 : min(n0 + kTN, n_out) - 1);

@@ -27,9 +27,11 @@ def _epilogue(lin: Lin, epilogue: str | None) -> tuple[int, int]:
         raise ValueError(f"Unknown epilogue {epilogue!r}; expected one of {EPILOGUES}")
     if epilogue is None:
         return 0, lin.out
-    if len(lin.sizes) != 2 or lin.sizes[0] != lin.sizes[1] or lin.sizes[0] % 128:
+    if len(lin.sizes) != 2 or lin.sizes[0] != lin.sizes[1] or lin.sizes[0] % 128 or lin.caps[0] != lin.caps[1] \
+            or lin.caps[0] > 64:
         raise ValueError(f"{', '.join(lin.names)}: the silu_mul epilogue takes a gate and an up matrix of one width, a "
-                         f"multiple of 128; got widths {lin.sizes}")
+                         f"multiple of 128, and one rank capacity of at most 64; got widths {lin.sizes}, capacities "
+                         f"{lin.caps}")
     return _lib.EPILOGUE_SILU_MUL, lin.sizes[0]
 
 

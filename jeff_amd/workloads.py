@@ -48,6 +48,7 @@ class Workload:
     adapter_ranks: dict[int, int]         # pool row -> rank of every adapted matrix
     gather_last: bool = False
     readout: dict | None = None           # decision head: readout_pool, temp_pool, counts (gather_last workloads)
+    gated: bool = False                   # gate_up is a gate and an up matrix of one width (SiLU(gate) * up applies)
     notes: dict = field(default_factory=dict)
 
 
@@ -147,7 +148,7 @@ def make(name: str, device: str = "cuda", seed: int = 0, n_layers: int | None = 
                     adp=torch.tensor(ids.astype(np.int32), device=device),
                     cu_seqlens=torch.tensor(cu, device=device) if ragged else None,
                     tokens=int(cu[-1]), requests=len(lengths), lengths=lengths, adapter_ranks=ranks,
-                    gather_last=gather, readout=readout)
+                    gather_last=gather, readout=readout, gated=name != "prefill-1layer")
 
 
 def inputs(w: Workload, label: str, gen: torch.Generator | None = None) -> torch.Tensor:
@@ -175,15 +176,16 @@ def flops_per_token(w: Workload) -> float:
     return total
 
 
-def hbm_bytes(w: Workload) -> float:
+def hbm_bytes(w: Workload, gated: tuple[str, ...] = ()) -> float:
     """Algorithmic HBM bytes of one pass: INT4 codes, scales and zero points of every group once, activations in and
-    out once, and the A and sB of every adapter present once (its live ranks only)."""
+    out once, and the A and sB of every adapter present once (its live ranks only). Groups named in `gated` write
+    silu(gate) * up, half their columns."""
     present = sorted({int(a) for a in token_ids(w)} - {0})
     total = 0.0
     for layer in w.layers:
-        for lin in layer.values():
+        for label, lin in layer.items():
             total += lin.int4.nbytes() if lin.int4 is not None else 0
-            total += 2.0 * w.tokens * (lin.k + lin.out)
+            total += 2.0 * w.tokens * (lin.k + (lin.out // 2 if label in gated else lin.out))
             for a in present:
                 r = w.adapter_ranks[a]
                 total += sum(2.0 * min(r, c) * (lin.k + n) for n, c in zip(lin.sizes, lin.caps) if c)
