@@ -382,8 +382,11 @@ __device__ __forceinline__ void finish_gated_columns(const mlora_lora_t& L, cons
   }
 }
 
+// (one input range: five waves per SIMD, as the plain form's 91 registers allow, so the loads of more segments are
+// in flight)
 template <int MAXS>
-__global__ __launch_bounds__(kFinThreads) void finish_gated_kernel(mlora_lora_t L, mlora_route_t r,
+__global__ __launch_bounds__(kFinThreads) __attribute__((amdgpu_waves_per_eu(MAXS == 1 ? 5 : 3))) void
+finish_gated_kernel(mlora_lora_t L, mlora_route_t r,
                                                                   const float* __restrict__ part, int32_t ksplit,
                                                                   int32_t ld, const uint16_t* __restrict__ mid,
                                                                   uint16_t* __restrict__ y, int64_t y_stride,
