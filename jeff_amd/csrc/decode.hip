@@ -397,8 +397,9 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const uint2 u = ex[((rg * kDMB + mb) * 4 + g) * 64 + lane];
-          const uint32_t lo = silu_mul2(pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]), u.x);
-          const uint32_t hi = silu_mul2(pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]), u.y);
+          const uint2 v = silu_mul4(make_uint2(pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]),
+                                               pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3])), u);
+          const uint32_t lo = v.x, hi = v.y;
           const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
           if (vec) {
             *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
@@ -517,8 +518,9 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_gated_kernel(const fl
     uv.z += b.z;
     uv.w += b.w;
   }
-  const uint32_t lo = silu_mul2(pack_bf16x2(gv.x, gv.y), pack_bf16x2(uv.x, uv.y));
-  const uint32_t hi = silu_mul2(pack_bf16x2(gv.z, gv.w), pack_bf16x2(uv.z, uv.w));
+  const uint2 v = silu_mul4(make_uint2(pack_bf16x2(gv.x, gv.y), pack_bf16x2(gv.z, gv.w)),
+                            make_uint2(pack_bf16x2(uv.x, uv.y), pack_bf16x2(uv.z, uv.w)));
+  const uint32_t lo = v.x, hi = v.y;
   const int64_t orig = r.tok_perm[row];
   const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
   if (vec) {

@@ -365,7 +365,7 @@ __device__ __forceinline__ void finish_gated_columns(const mlora_lora_t& L, cons
     if (h == 0 && srow < rows) {
       const uint2 g = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
       const uint2 u = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + 128 + scol]);
-      const uint2 v = make_uint2(silu_mul2(g.x, u.x), silu_mul2(g.y, u.y));
+      const uint2 v = silu_mul4(g, u);
       const int c = c0 + scol;
       uint16_t* yrow = y + yrow_off;
       if (vec) {

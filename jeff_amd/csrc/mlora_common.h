@@ -67,18 +67,38 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-// The gated activation of two packed bf16 pairs (the reference's silu_mul, engine/fast_path.py:141-156): for gate g and
-// up u, bf16(bf16(g / (1 + exp(-g))) u), lo and hi halves independently. Shared by silu_mul_kernel and the products
-// that apply it in their output tiles, so both give the same bits.
-__device__ __forceinline__ float silu_bf16(float g) {
-  const float v = g / (1.0f + __expf(-g));
+// The gated activation of packed bf16 values (the reference's silu_mul, engine/fast_path.py:141-156): for gate g and
+// up u, bf16(bf16(g / (1 + exp(-g))) u), each value independently. Shared by silu_mul_kernel and the products that
+// apply it in their output tiles, so both give the same bits. The quotient g / d is the hardware reciprocal's q0 =
+// g rcp(d) corrected once by its exact residual (fma(-q0, d, g), exact while q0 is within a few ulps of g / d):
+// q0 + residual rcp(d), rounded once, is the correctly rounded quotient except within about 2^-22 ulp of a rounding
+// boundary (a bare reciprocal, within 1 ulp, misrounds values within an ulp of a bf16 rounding midpoint). Where d
+// reaches 2^120 (g below about -83: the reciprocal would fall among the denormals, which it flushes) the quotient is
+// an IEEE division.
+__device__ __forceinline__ float bf16_round(float v) {
   return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v) << 16);
 }
-__device__ __forceinline__ uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
-  return pack_bf16x2(silu_bf16(bf16_lo(g2)) * bf16_lo(u2), silu_bf16(bf16_hi(g2)) * bf16_hi(u2));
+__device__ __forceinline__ float silu_quotient(float g) {
+  const float d = 1.0f + __expf(-g);
+  if (__builtin_expect(!(d < 0x1p120f), 0)) return g / d;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q0 = g * r;
+  return __builtin_fmaf(__builtin_fmaf(-q0, d, g), r, q0);
 }
 __device__ __forceinline__ uint4 silu_mul8(uint4 g, uint4 u) {
-  return make_uint4(silu_mul2(g.x, u.x), silu_mul2(g.y, u.y), silu_mul2(g.z, u.z), silu_mul2(g.w, u.w));
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float g0 = bf16_lo(gw[e]), g1 = bf16_hi(gw[e]);
+    o[e] = pack_bf16x2(bf16_round(silu_quotient(g0)) * bf16_lo(uw[e]), bf16_round(silu_quotient(g1)) * bf16_hi(uw[e]));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+// four values (two packed pairs each of gate and up)
+__device__ __forceinline__ uint2 silu_mul4(uint2 g, uint2 u) {
+  const uint4 v = silu_mul8(make_uint4(g.x, g.y, 0, 0), make_uint4(u.x, u.y, 0, 0));
+  return make_uint2(v.x, v.y);
 }
 
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
