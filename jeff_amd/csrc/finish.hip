@@ -366,7 +366,10 @@ __device__ __forceinline__ void finish_gated_columns(const mlora_lora_t& L, cons
       const uint2 g = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
       const uint2 u = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + 128 + scol]);
       const uint2 v = silu_mul4(g, u);
-      const int c = c0 + scol;
+      // (the column offset is opaque so the output addresses are formed here: hoisted out of the row loop, the
+      // last-token row's 64-bit address did not fit the registers and went to scratch memory, once per thread)
+      int c = c0 + scol;
+      asm volatile("" : "+v"(c));
       uint16_t* yrow = y + yrow_off;
       if (vec) {
         *reinterpret_cast<uint2*>(yrow + c) = v;

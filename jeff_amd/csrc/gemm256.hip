@@ -200,25 +200,29 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // the tile's first matrix.
   const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
   const int jlo = lora ? matrix_of(L, GATED ? nt * 128 : n0) : 0;
-  int s_lo = 0, s_hi = -1, a_pre[2] = {0, 0}, live_pre[2] = {0, 0}, live_up[2] = {0, 0};
+  // (each pair packed in one 64-bit word, segment s_lo's in the low half: an array indexed by the segment would be
+  // placed in scratch memory)
+  int s_lo = 0, s_hi = -1;
+  uint64_t a_pre = 0, live_pre = 0, live_up = 0;
   if (lora) {
     auto sload = [](const int32_t* q, int64_t i) __attribute__((always_inline)) {
       return ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)q)[i];
     };
     s_lo = sload(r.seg_of, p0);
     s_hi = sload(r.seg_of, min(p0 + kRows, T) - 1);
-    a_pre[0] = sload(r.seg_adapter, s_lo);
-    a_pre[1] = sload(r.seg_adapter, min(s_lo + 1, s_hi));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int rk = a_pre[u] == 0 ? 0 : sload(L.ranks, (int64_t)a_pre[u] * L.ranks_stride + jlo);
-      live_pre[u] = min(max(rk, 0), L.cap[jlo]);
+      const int a = sload(r.seg_adapter, u == 0 ? s_lo : min(s_lo + 1, s_hi));
+      const int rk = a == 0 ? 0 : sload(L.ranks, (int64_t)a * L.ranks_stride + jlo);
+      a_pre |= (uint64_t)(uint32_t)a << (32 * u);
+      live_pre |= (uint64_t)(uint32_t)min(max(rk, 0), L.cap[jlo]) << (32 * u);
       if constexpr (GATED) {  // and of the up matrix, which waves 4..7 add
-        const int ru = a_pre[u] == 0 ? 0 : sload(L.ranks, (int64_t)a_pre[u] * L.ranks_stride + 1);
-        live_up[u] = min(max(ru, 0), L.cap[1]);
+        const int ru = a == 0 ? 0 : sload(L.ranks, (int64_t)a * L.ranks_stride + 1);
+        live_up |= (uint64_t)(uint32_t)min(max(ru, 0), L.cap[1]) << (32 * u);
       }
     }
   }
+  auto half_of = [](uint64_t pair, int i) __attribute__((always_inline)) { return (int)(uint32_t)(pair >> (32 * i)); };
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
   load_a(g_x0, 0, a);
@@ -309,8 +313,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
         int a, live;
         if (s - s_lo < 2) {  // read ahead in the prologue
-          a = a_pre[s - s_lo];
-          live = j == 0 ? live_pre[s - s_lo] : live_up[s - s_lo];
+          a = half_of(a_pre, s - s_lo);
+          live = half_of(j == 0 ? live_pre : live_up, s - s_lo);
         } else {
           a = r.seg_adapter[s];
           live = a == 0 ? 0 : live_rank(L, a, j);
@@ -383,8 +387,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
           int a, live;
           if (j == jlo && s - s_lo < 2) {  // read ahead
-            a = a_pre[s - s_lo];
-            live = live_pre[s - s_lo];
+            a = half_of(a_pre, s - s_lo);
+            live = half_of(live_pre, s - s_lo);
           } else {
             a = r.seg_adapter[s];
             live = a == 0 ? 0 : live_rank(L, a, j);
