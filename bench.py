@@ -121,7 +121,7 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
     import torch
 
     from jeff_amd import workloads
-    from jeff_amd.epilogues import add_rms, silu_mul
+    from jeff_amd.epilogues import add_rms, rms, silu_mul
     from jeff_amd.fast_path import DT, Workspace
     from jeff_amd.int4_kernels import base_expand, int4_product, shrink
     from jeff_amd import _lib
@@ -267,6 +267,32 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
                                     "hbm_bytes_saved": 2.0 * w.tokens * inter * 4,
                                     "note": "the plain product writes 2 inter columns, silu_mul reads them and writes "
                                             "inter; the fused product writes inter columns once"}
+
+    if w.gated:
+        # the residual add in the down product's output tile, then the RMSNorm of the sums, against the plain product
+        # followed by add_rms (which adds and normalises): the whole down product each way (first factor included)
+        dl = w.layers[0]["down"]
+        dx = xs[(0, "down")]
+        rg = torch.Generator(device="cuda").manual_seed(78)
+        resid0 = torch.randn(w.tokens, dl.out, device=dev, generator=rg).to(DT)
+        resid = resid0.clone()
+        nw = (1 + 0.1 * torch.randn(dl.out, device=dev, generator=rg)).float()
+        d_reps = max(3, min(100, int(reps * lin.out * lin.k / (dl.out * dl.k))))
+
+        def fused_down() -> None:  # (the residual grows by the product each repetition: timing only)
+            int4_product(dl, dx, ws, w.adp, epilogue="residual", residual=resid)
+            rms(resid, nw)
+
+        plain = capture(lambda: add_rms(resid0, int4_product(dl, dx, ws, w.adp), nw), d_reps)
+        fused = capture(fused_down, d_reps)
+        plain_ms, fused_ms = replay_ms(plain, stream, d_reps), replay_ms(fused, stream, d_reps)
+        del plain, fused, resid, resid0
+        result["fused_residual_add"] = {"group": "layer0.down", "plain_product_and_add_rms_ms": plain_ms,
+                                        "fused_product_and_rms_ms": fused_ms,
+                                        "hbm_bytes_saved": 2.0 * w.tokens * dl.out * 2,
+                                        "note": "the plain product writes d, add_rms reads x and d and writes x + d "
+                                                "and the norm; the fused product reads x and writes x + d in its "
+                                                "output tile, rms reads x + d and writes the norm"}
 
     if w.readout is not None:  # the decision head alone: its two launches, timed as the dominant kernel is
         r = w.readout

@@ -80,6 +80,13 @@ enum {
  * the unfused product. Products with this flag never take the GEMV kernel; the split product needs capacities in
  * {0, 8, 16, 32, 64}; mlora_lora_add refuses it. */
 #define MLORA_EPILOGUE_SILU_MUL 64
+/* Epilogue flag: the residual add of add_rms (fast_path.py:80-100, x = bf16(x + d)) in the product's output tile. y
+ * holds the residual rows on entry (row t at y + t * y_stride) and receives bf16(residual + output) with the output
+ * rounded to bf16 first, the bits mlora_add_rms writes for x + d on the unfused product; last_out (when given)
+ * receives the same sums. y must not overlap x. Not with MLORA_EPILOGUE_SILU_MUL (MLORA_EINVAL); products with this
+ * flag never take the GEMV kernel; the fused product needs tokens * max(x_stride, k) below 2^31 and the split product
+ * capacities in {0, 8, 16, 32, 64} (MLORA_EUNSUPPORTED otherwise); mlora_lora_add refuses it. */
+#define MLORA_EPILOGUE_RESIDUAL 128
 
 /* INT4 weights in the kernel layout (reference int4.py:215-230, plus zero points and g128):
  * words  int32 (k/8, columns): word i of column c holds inputs 8i..8i+7, input 8i+j in bits 4j..4j+3 (the code c);

@@ -99,10 +99,13 @@ bool split_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_
 int32_t gated_width(const mlora_int4_t* w, int32_t flags) {
   return (flags & MLORA_EPILOGUE_SILU_MUL) ? w->out / 2 : 0;
 }
+// The residual epilogue (MLORA_EPILOGUE_RESIDUAL): y holds the residual and receives residual + output.
+bool residual_of(int32_t flags) { return (flags & MLORA_EPILOGUE_RESIDUAL) != 0; }
 
 int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
             Base* out) {
-  const bool gated = (flags & MLORA_EPILOGUE_SILU_MUL) != 0;
+  const bool gated = (flags & MLORA_EPILOGUE_SILU_MUL) != 0, resid = residual_of(flags);
+  if (gated && resid) return MLORA_EINVAL;  // one epilogue per product
   const int32_t fs = (flags >> 8) & 0xF;
   if (fs != 0 && (!(fs == 1 || fs == 2 || fs == 4 || fs == 8) || (w->k / 64) % fs)) return MLORA_EUNSUPPORTED;
   if (flags & MLORA_FORCE_BASE_GEMV) {
@@ -116,7 +119,7 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
     *out = Base::narrow;
   } else if (flags & MLORA_FORCE_BASE_MFMA) {
     *out = Base::fused;
-  } else if (r->tokens <= 8 && !gated) {  // (the GEMV kernel has no gated epilogue: few tokens take the tiles)
+  } else if (r->tokens <= 8 && !gated && !resid) {  // (the GEMV kernel has no epilogues: few tokens take the tiles)
     *out = Base::gemv;
   } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
     *out = Base::fused;
@@ -132,6 +135,13 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
         L->cap[0] != L->cap[1] || L->cap[0] > 64)
       return MLORA_EUNSUPPORTED;
     const int64_t row = x_stride > w->k ? x_stride : w->k;
+    if (*out == Base::fused && r->tokens > 0 && row >= ((int64_t)1 << 31) / r->tokens) return MLORA_EUNSUPPORTED;
+    if (*out == Base::split && !finish_registers(*L)) return MLORA_EUNSUPPORTED;
+  }
+  if (resid) {
+    // the 256 x 256 kernel for the fused product, the register form of the split epilogue
+    const int64_t row = x_stride > w->k ? x_stride : w->k;
+    if (*out == Base::gemv) return MLORA_EUNSUPPORTED;
     if (*out == Base::fused && r->tokens > 0 && row >= ((int64_t)1 << 31) / r->tokens) return MLORA_EUNSUPPORTED;
     if (*out == Base::split && !finish_registers(*L)) return MLORA_EUNSUPPORTED;
   }
@@ -192,15 +202,16 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
              void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
   const int32_t inter = gated_width(w, flags);
+  const bool resid = residual_of(flags);
   if (base == Base::narrow) {
     const int32_t ks = narrow_ranges(w, flags);
     const size_t need = dec_partials_bytes(*w, ks);
     if (need > 0 && (partials == nullptr || !aligned16(partials) || partials_bytes < need)) return MLORA_EWORKSPACE;
     return launch_dec(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, static_cast<float*>(partials), ks,
-                      s, inter);
+                      s, inter, resid);
   }
-  if (base == Base::fused && inter > 0)
-    return launch_base256(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, nullptr, 1, s, inter);
+  if (base == Base::fused && (inter > 0 || resid))
+    return launch_base256(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, nullptr, 1, s, inter, resid);
   if (base != Base::split)
     return launch_base(w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, base == Base::gemv, s);
   if (partials == nullptr || !aligned16(partials) || partials_bytes < split_bytes(w, r->tokens))
@@ -209,7 +220,7 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
   float* part = static_cast<float*>(partials);
   int rc = launch_base256(*w, *L, *r, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s);
   if (rc) return rc;
-  return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s, inter);
+  return launch_finish(*L, *r, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s, inter, resid);
 }
 
 // The device address of `scratch` on the current device, looked up once per device (with that device current);
@@ -353,7 +364,7 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
       return rc;
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s,
-                         gated_width(w, flags));
+                         gated_width(w, flags), residual_of(flags));
   }
   if (base == Base::split) {
     // split product of long segments (forced): the first factor, the base ranges, then the epilogue
@@ -363,7 +374,7 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     if ((rc = launch_base256(*w, *lora, *route, x, x_stride, nullptr, 0, nullptr, w->out, nullptr, part, ks, s)))
       return rc;
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s,
-                         gated_width(w, flags));
+                         gated_width(w, flags), residual_of(flags));
   }
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
   return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
@@ -418,7 +429,8 @@ int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const u
   if (y == nullptr || y_stride < n_out) return MLORA_EINVAL;
   if (workspace == nullptr || !aligned16(workspace)) return MLORA_EWORKSPACE;
   if (workspace_bytes < mlora_workspace_bytes(route->tokens, lora->rank_cap)) return MLORA_EWORKSPACE;
-  if (flags & (MLORA_FORCE_BASE_SPLIT | MLORA_EPILOGUE_SILU_MUL)) return MLORA_EUNSUPPORTED;  // y is updated in place
+  if (flags & (MLORA_FORCE_BASE_SPLIT | MLORA_EPILOGUE_SILU_MUL | MLORA_EPILOGUE_RESIDUAL))
+    return MLORA_EUNSUPPORTED;  // y is updated in place
   const bool gemv = (flags & MLORA_FORCE_BASE_GEMV) || (!(flags & MLORA_FORCE_BASE_MFMA) && route->tokens <= 8);
   if (gemv && route->tokens > 8) return MLORA_EUNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);

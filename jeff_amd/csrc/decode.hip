@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
                                                pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3])), u);
           const uint32_t lo = v.x, hi = v.y;
           const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
-          if (vec) {
+          if (vec & kStoreVec) {
             *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
             if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
           } else {
@@ -427,18 +427,9 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     for (int g = 0; g < 4; ++g) {
       const int col = cw0 + g * 8 + (lane >> 5) * 4;
       if (col >= n_out) continue;
-      const uint32_t lo = pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]);
-      const uint32_t hi = pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
-      if (vec && col + 3 < n_out) {
-        *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
-        if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * n_out + col) = make_uint2(lo, hi);
-      } else {
-        const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
-        for (int e = 0; e < 4 && col + e < n_out; ++e) {
-          y[orig * y_stride + col + e] = h[e];
-          if (lq >= 0) last_out[lq * n_out + col + e] = h[e];
-        }
-      }
+      store4(y + orig * y_stride + col, lq >= 0 ? last_out + lq * n_out + col : nullptr,
+             pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]), pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]),
+             n_out - col, vec);
     }
   }
 }
@@ -469,19 +460,10 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_kernel(const float4* 
     v.z += u.z;
     v.w += u.w;
   }
-  const uint32_t lo = pack_bf16x2(v.x, v.y), hi = pack_bf16x2(v.z, v.w);
   const int64_t orig = r.tok_perm[row];
   const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
-  if (vec && col + 3 < n_out) {
-    *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
-    if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * n_out + col) = make_uint2(lo, hi);
-  } else {
-    const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
-    for (int e = 0; e < 4 && col + e < n_out; ++e) {
-      y[orig * y_stride + col + e] = h[e];
-      if (lq >= 0) last_out[lq * n_out + col + e] = h[e];
-    }
-  }
+  store4(y + orig * y_stride + col, lq >= 0 ? last_out + lq * n_out + col : nullptr, pack_bf16x2(v.x, v.y),
+         pack_bf16x2(v.z, v.w), n_out - col, vec);
 }
 
 // The same for a gated product: thread f takes float4 f of the gate waves' partial tiles (column group 0 of every row
@@ -523,7 +505,7 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_gated_kernel(const fl
   const uint32_t lo = v.x, hi = v.y;
   const int64_t orig = r.tok_perm[row];
   const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
-  if (vec) {
+  if (vec & kStoreVec) {
     *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
     if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
   } else {
@@ -544,31 +526,34 @@ size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit) {
 
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter) {
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter, bool residual) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
-  if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit) return MLORA_EINVAL;
+  if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit || (residual && inter > 0)) return MLORA_EINVAL;
   if (inter > 0 && (inter % 32 || n_out != 2 * inter)) return MLORA_EINVAL;
   if (ksplit > 1 && part == nullptr) return MLORA_EWORKSPACE;
   const int n_tiles = inter > 0 ? inter / 32 : w.columns / kDCols;
   const int out_cols = inter > 0 ? inter : n_out;  // columns of y and last_out
   // 8-byte stores of four columns need 8-byte aligned output rows
-  const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
-                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && out_cols % 4 == 0));
+  const int32_t vec = (reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
+                       (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && out_cols % 4 == 0))
+                           ? kStoreVec
+                           : 0) |
+                      (residual ? kStoreResidual : 0);
   float4* p4 = reinterpret_cast<float4*>(part);
   hipLaunchKernelGGL(inter > 0 ? dec_kernel<true> : dec_kernel<false>, dim3((unsigned)(n_tiles * ksplit)),
                      dim3(kDThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, n_tiles,
-                     (int32_t)vec, p4, ksplit, inter);
+                     vec, p4, ksplit, inter);
   if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
   if (ksplit > 1) {
     const int64_t per = (int64_t)n_tiles * kDRows * kDCols / 4;
     if (inter > 0)
       hipLaunchKernelGGL(dec_reduce_gated_kernel, dim3((unsigned)((per / 2 + kDRedThreads - 1) / kDRedThreads)),
                          dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, inter,
-                         (int32_t)vec);
+                         vec);
     else
       hipLaunchKernelGGL(dec_reduce_kernel, dim3((unsigned)((per + kDRedThreads - 1) / kDRedThreads)),
                          dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, n_out,
-                         (int32_t)vec);
+                         vec);
     if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
   }
   return MLORA_OK;

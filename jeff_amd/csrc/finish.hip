@@ -163,7 +163,8 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
                                                const uint16_t* __restrict__ mid, uint16_t* __restrict__ y,
                                                int64_t y_stride, uint16_t* __restrict__ last_out, int32_t n_out,
                                                int64_t sb, int64_t se, int a, int j, int oj, int c0, int ncols,
-                                               bool vec, float* __restrict__ base_lds, uint16_t* __restrict__ out_lds) {
+                                               int32_t vec, float* __restrict__ base_lds,
+                                               uint16_t* __restrict__ out_lds) {
   const int tid = threadIdx.x;
   const int ch = tid % CPC, cl = tid / CPC;
   const int rk = a != 0 ? live_rank(L, a, j) : 0;
@@ -229,17 +230,7 @@ __device__ __forceinline__ void finish_columns(const mlora_lora_t& L, const mlor
     if (srow < rows && scol < ncols) {
       const int c = oj + c0 + scol;
       const uint2 v = *reinterpret_cast<const uint2*>(&out_lds[srow * kFinThreads + scol]);
-      uint16_t* yrow = y + yrow_off;
-      if (vec && scol + 4 <= ncols) {
-        *reinterpret_cast<uint2*>(yrow + c) = v;
-        if (q >= 0) *reinterpret_cast<uint2*>(last_out + (int64_t)q * n_out + c) = v;
-      } else {
-        const uint16_t h[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
-        for (int e = 0; e < 4 && scol + e < ncols; ++e) {
-          yrow[c + e] = h[e];
-          if (q >= 0) last_out[(int64_t)q * n_out + c + e] = h[e];
-        }
-      }
+      store4(y + yrow_off + c, q >= 0 ? last_out + (int64_t)q * n_out + c : nullptr, v.x, v.y, ncols - scol, vec);
     }
   }
 }
@@ -273,19 +264,19 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(mlora_lora_t L, mlo
   switch (sb_stride(a != 0 ? live_rank(L, a, j) : 0, L.cap[j])) {  // the adapter's sB row stride
     case 64:
       finish_columns<8, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
-                        vec != 0, base_lds, out_lds);
+                        vec, base_lds, out_lds);
       break;
     case 32:
       finish_columns<4, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
-                        vec != 0, base_lds, out_lds);
+                        vec, base_lds, out_lds);
       break;
     case 16:
       finish_columns<2, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
-                        vec != 0, base_lds, out_lds);
+                        vec, base_lds, out_lds);
       break;
     default:  // 8, or 0 (no adapter on this matrix: the base partial sums only)
       finish_columns<1, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, n_out, sb, se, a, j, oj, c0, ncols,
-                        vec != 0, base_lds, out_lds);
+                        vec, base_lds, out_lds);
       break;
   }
 }
@@ -408,19 +399,19 @@ finish_gated_kernel(mlora_lora_t L, mlora_route_t r,
   switch (max(sg, su)) {  // the larger sB row stride of the two matrices
     case 64:
       finish_gated_columns<8, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
-                                    vec != 0, base_lds, out_lds);
+                                    vec, base_lds, out_lds);
       break;
     case 32:
       finish_gated_columns<4, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
-                                    vec != 0, base_lds, out_lds);
+                                    vec, base_lds, out_lds);
       break;
     case 16:
       finish_gated_columns<2, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
-                                    vec != 0, base_lds, out_lds);
+                                    vec, base_lds, out_lds);
       break;
     default:
       finish_gated_columns<1, MAXS>(L, r, part, ksplit, ld, mid, y, y_stride, last_out, inter, sb, se, a, c0,
-                                    vec != 0, base_lds, out_lds);
+                                    vec, base_lds, out_lds);
       break;
   }
 }
@@ -438,9 +429,10 @@ bool finish_registers(const mlora_lora_t& L) {
 
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                  hipStream_t stream, int32_t inter) {
+                  hipStream_t stream, int32_t inter, bool residual) {
   if (r.tokens == 0 || n_out == 0 || r.max_segs == 0) return MLORA_OK;
   if (inter > 0) {
+    if (residual) return MLORA_EINVAL;
     if (inter % 128 || L.n_mats != 2 || L.cols[0] != inter || L.cols[1] != inter || !finish_registers(L))
       return MLORA_EINVAL;
     const dim3 grid((unsigned)(inter / 128), (unsigned)r.max_segs);
@@ -458,17 +450,22 @@ int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* pa
   // the register form: every cap_j in {0, 8, 16, 32, 64} and every matrix a multiple of four columns (its partial
   // sums are read four columns at a time)
   const bool registers = finish_registers(L);
+  if (residual && !registers) return MLORA_EINVAL;
   for (int j = 0; j < L.n_mats; ++j) blocks += (L.cols[j] + kFinThreads - 1) / kFinThreads;
   const dim3 grid((unsigned)blocks, (unsigned)r.max_segs);
   // 8-byte stores of four columns: 8-byte aligned output rows
-  const bool vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
-                   (last_out == nullptr || (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0));
+  const int32_t vec = (reinterpret_cast<uintptr_t>(y) % 8 == 0 && y_stride % 4 == 0 &&
+                               (last_out == nullptr ||
+                                (reinterpret_cast<uintptr_t>(last_out) % 8 == 0 && n_out % 4 == 0))
+                           ? kStoreVec
+                           : 0) |
+                      (residual ? kStoreResidual : 0);
   if (registers && ksplit == 1)
     hipLaunchKernelGGL(finish_kernel<1>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y, y_stride,
-                       last_out, n_out, (int32_t)vec);
+                       last_out, n_out, vec);
   else if (registers)
     hipLaunchKernelGGL(finish_kernel<kMaxSplit>, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
-                       y_stride, last_out, n_out, (int32_t)vec);
+                       y_stride, last_out, n_out, vec);
   else
     hipLaunchKernelGGL(finish_lds_kernel, grid, dim3(kFinThreads), 0, stream, L, r, part, ksplit, ld, mid, y,
                        y_stride, last_out, n_out);

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
                                                                uint16_t* __restrict__ last_out, int32_t n_out,
-                                                               const uint16_t* __restrict__ mid, int32_t n_tiles, int32_t vec,
+                                                               const uint16_t* __restrict__ mid, int32_t n_tiles,
+                                                               int32_t vec,  // kStoreVec | kStoreResidual
                                                                float* __restrict__ part, int32_t ksplit,
                                                                int32_t base_blocks, int32_t inter) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       const int off = row * 128 + ((c ^ (row & 15)) << 3);
       const uint4 v = silu_mul8(*reinterpret_cast<const uint4*>(&gb[off]), *reinterpret_cast<const uint4*>(&ub[off]));
       const int col = nt * 128 + c * 8;
-      if (vec) {
+      if (vec & kStoreVec) {
         *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
         if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * inter + col) = v;
       } else {
@@ -501,16 +502,22 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     if (orig < 0) continue;
     const int64_t lq = g_last[half * 128 + row];
     const uint16_t* buf = half == 0 ? (bsel ? g_x1 : g_x0) : (bsel ? g_x3 : g_x2);
-    const uint4 v = *reinterpret_cast<const uint4*>(&buf[row * 128 + ((c ^ (row & 15)) << 3)]);
+    uint4 v = *reinterpret_cast<const uint4*>(&buf[row * 128 + ((c ^ (row & 15)) << 3)]);
     const int col = n0 + bsel * 128 + c * 8;
-    if (vec && col + 7 < n_out) {
-      *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
+    uint16_t* yr = y + orig * y_stride + col;
+    if ((vec & kStoreVec) && col + 7 < n_out) {
+      if (vec & kStoreResidual) {  // the output row holds the residual: bf16(residual + output)
+        const uint4 rv = *reinterpret_cast<const uint4*>(yr);
+        v = make_uint4(add_bf16x2(rv.x, v.x), add_bf16x2(rv.y, v.y), add_bf16x2(rv.z, v.z), add_bf16x2(rv.w, v.w));
+      }
+      *reinterpret_cast<uint4*>(yr) = v;
       if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * n_out + col) = v;
     } else {
       const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
       for (int e = 0; e < 8 && col + e < n_out; ++e) {
-        const uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
-        y[orig * y_stride + col + e] = h;
+        uint16_t h = (uint16_t)(e4[e >> 1] >> (16 * (e & 1)));
+        if (vec & kStoreResidual) h = add_bf16(yr[e], h);
+        yr[e] = h;
         if (lq >= 0) last_out[lq * n_out + col + e] = h;
       }
     }
@@ -538,7 +545,9 @@ int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
 
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter) {
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter,
+                   bool residual) {
+  if (residual && (inter > 0 || part != nullptr)) return MLORA_EINVAL;
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
   if (inter > 0 && (part != nullptr || inter % 128 || n_out != 2 * inter)) return MLORA_EINVAL;
   const int n_tiles = inter > 0 ? inter / 128 : (n_out + kTN - 1) / kTN;
@@ -552,6 +561,7 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
   auto kernel = inter > 0 ? (mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
                           : (mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid,
-                     n_tiles, (int32_t)vec, part, ksplit, (int32_t)blocks, inter);
+                     n_tiles, (vec ? kStoreVec : 0) | (residual ? kStoreResidual : 0), part, ksplit, (int32_t)blocks,
+                     inter);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

@@ -101,6 +101,42 @@ __device__ __forceinline__ uint2 silu_mul4(uint2 g, uint2 u) {
   return make_uint2(v.x, v.y);
 }
 
+// The residual add of add_rms (engine/fast_path.py:87-89: x = bf16(x + d)) on packed bf16 pairs: r the residual, v
+// the product's output, already rounded once to bf16; the float32 sum rounded to bf16.
+__device__ __forceinline__ uint32_t add_bf16x2(uint32_t r, uint32_t v) {
+  return pack_bf16x2(bf16_lo(r) + bf16_lo(v), bf16_hi(r) + bf16_hi(v));
+}
+__device__ __forceinline__ uint16_t add_bf16(uint16_t r, uint16_t v) {
+  return (uint16_t)add_bf16x2(r, v);
+}
+
+// Output flags the store paths of the product kernels take in one word: bit 0 whole-vector stores are aligned, bit 1
+// the residual add (the output rows hold the residual on entry and receive bf16(residual + output)).
+constexpr int32_t kStoreVec = 1, kStoreResidual = 2;
+
+// Four consecutive output columns of one row (two packed bf16 pairs lo, hi) to y at yr and, when `last` is not null,
+// to the request's last-token row; `left` columns of the row remain from the first. With kStoreResidual the four
+// values written are bf16(yr[e] + value), read from the row first.
+__device__ __forceinline__ void store4(uint16_t* yr, uint16_t* last, uint32_t lo, uint32_t hi, int left,
+                                       int32_t flags) {
+  if ((flags & kStoreVec) && left >= 4) {
+    if (flags & kStoreResidual) {
+      const uint2 rv = *reinterpret_cast<const uint2*>(yr);
+      lo = add_bf16x2(rv.x, lo);
+      hi = add_bf16x2(rv.y, hi);
+    }
+    *reinterpret_cast<uint2*>(yr) = make_uint2(lo, hi);
+    if (last != nullptr) *reinterpret_cast<uint2*>(last) = make_uint2(lo, hi);
+  } else {
+    const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+    for (int e = 0; e < 4 && e < left; ++e) {
+      const uint16_t v = (flags & kStoreResidual) ? add_bf16(yr[e], h[e]) : h[e];
+      yr[e] = v;
+      if (last != nullptr) last[e] = v;
+    }
+  }
+}
+
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
@@ -190,22 +226,25 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
                   uint16_t* mid, bool mfma, hipStream_t stream);
 // 256 x 256 tiles; with part != nullptr the split mode: ksplit input ranges, float32 sums to part, nothing else.
 // inter > 0: a gated product (the group is gate and up, inter columns each; y and last_out receive silu(gate) * up,
-// inter columns), fused mode only.
+// inter columns), fused mode only. residual: y holds the residual rows on entry and receives bf16(residual + output)
+// (last_out the same sums), fused mode and not gated.
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                    int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0);
+                   const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
+                   bool residual = false);
 // The second launch of a split product: partial sums in order + LoRA term, rounded once (inter > 0: gated, as above;
-// the register form's capacities only, finish_registers).
+// the register form's capacities only, finish_registers; residual as above, the register form only, not gated).
 bool finish_registers(const mlora_lora_t& L);
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                  hipStream_t stream, int32_t inter = 0);
+                  hipStream_t stream, int32_t inter = 0, bool residual = false);
 // Narrow product (every token, at most 256, in one row tile of 64 columns): ksplit input ranges; with ksplit > 1
-// part holds dec_partials_bytes(w, ksplit) and a second launch adds the ranges.
+// part holds dec_partials_bytes(w, ksplit) and a second launch adds the ranges (residual as above, not gated).
 size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit);
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0);
+               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
+               bool residual = false);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

@@ -18,7 +18,7 @@ from jeff_amd.fast_path import DT, Lin, Workspace, _check_input
 from jeff_amd.int4_tiles import Int4Tiles
 
 
-EPILOGUES = (None, "silu_mul")
+EPILOGUES = (None, "silu_mul", "residual")
 
 
 def _epilogue(lin: Lin, epilogue: str | None) -> tuple[int, int]:
@@ -27,6 +27,8 @@ def _epilogue(lin: Lin, epilogue: str | None) -> tuple[int, int]:
         raise ValueError(f"Unknown epilogue {epilogue!r}; expected one of {EPILOGUES}")
     if epilogue is None:
         return 0, lin.out
+    if epilogue == "residual":
+        return _lib.EPILOGUE_RESIDUAL, lin.out
     if len(lin.sizes) != 2 or lin.sizes[0] != lin.sizes[1] or lin.sizes[0] % 128 or lin.caps[0] != lin.caps[1] \
             or lin.caps[0] > 64:
         raise ValueError(f"{', '.join(lin.names)}: the silu_mul epilogue takes a gate and an up matrix of one width, a "
@@ -35,13 +37,37 @@ def _epilogue(lin: Lin, epilogue: str | None) -> tuple[int, int]:
     return _lib.EPILOGUE_SILU_MUL, lin.sizes[0]
 
 
+def _residual_rows(lin: Lin, x: torch.Tensor, residual: torch.Tensor | None, epilogue: str | None,
+                   m: int) -> None:
+    """ValueError unless `residual` is given exactly for epilogue="residual", as bf16 (m, lin.out) rows that do not
+    overlap x (the kernels read x while other tiles write the sums)."""
+    if (epilogue == "residual") != (residual is not None):
+        raise ValueError("epilogue='residual' takes the residual rows (residual=...), and no other epilogue does")
+    if residual is None:
+        return
+    if residual.dtype != DT or residual.dim() != 2 or tuple(residual.shape) != (m, lin.out) or \
+            residual.stride(1) != 1 or residual.device != x.device:
+        raise ValueError(f"residual must be a bfloat16 ({m}, {lin.out}) tensor with contiguous rows on {x.device}")
+
+    def span(t: torch.Tensor) -> tuple[int, int]:
+        return t.data_ptr(), t.data_ptr() + ((t.shape[0] - 1) * t.stride(0) + t.shape[1]) * t.element_size()
+
+    (a0, a1), (b0, b1) = span(x), span(residual)
+    if a0 < b1 and b0 < a1:
+        raise ValueError("residual must not overlap x")
+
+
 def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, tiles: Int4Tiles | None = None,
-                 last_out: torch.Tensor | None = None, epilogue: str | None = None) -> torch.Tensor:
+                 last_out: torch.Tensor | None = None, epilogue: str | None = None,
+                 residual: torch.Tensor | None = None) -> torch.Tensor:
     """The fused product of x (M, in) through `lin`'s INT4 weights plus each token's adapter update (the pool row of
     its request row in adp, or the route ws.route made). `tiles` forces the kernel families (tests); `last_out`
     (requests, columns) bf16 also receives each request's last-token output row. epilogue="silu_mul" (a gate_up
     group: gate then up, one width each): the result is silu_mul of the product, (M, width) (the reference's
-    silu_mul(product(...)), engine/batched_path.py:271, in the product's own output tile, bit for bit)."""
+    silu_mul(product(...)), engine/batched_path.py:271, in the product's own output tile, bit for bit).
+    epilogue="residual" with residual=r, (M, out) bf16: the residual add of add_rms in the output tile, r updated in
+    place to bf16(r + product) and returned (the x of the reference's add_rms(x, product(...), w),
+    engine/fast_path.py:80-100, bit for bit; the last-token rows receive the sums)."""
     packed = lin.int4
     if packed is None:
         raise ValueError(f"{', '.join(lin.names)}: no INT4 weights (attach_int4 gives them to an INT4 base's fused "
@@ -58,8 +84,9 @@ def int4_product(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, ti
     if last_out is not None and (last_out.dtype != DT or last_out.dim() != 2 or last_out.shape[1] != cols
                                  or not last_out.is_contiguous() or last_out.shape[0] < adp.numel()):
         raise ValueError(f"last_out must be a contiguous bfloat16 (requests, {cols}) tensor")
+    _residual_rows(lin, x, residual, epilogue, m)
     r = ws.routed(adp, lin.pool.shape[0], m)
-    y = torch.empty(m, cols, device=x.device, dtype=DT)
+    y = residual if residual is not None else torch.empty(m, cols, device=x.device, dtype=DT)
     h = _lib.lib()
     flags = (0 if tiles is None else tiles.flags()) | eflag
     w, lora = packed.abi(), lin.lora_abi()
@@ -90,7 +117,8 @@ def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: 
                 tiles: Int4Tiles | None = None, last_out: torch.Tensor | None = None,
                 epilogue: str | None = None) -> torch.Tensor:
     """int4_product without its first launch, into a given y: the base product and the LoRA second factor, reading
-    the first factors the last shrink (or int4_product) of the same x and adp left in the workspace."""
+    the first factors the last shrink (or int4_product) of the same x and adp left in the workspace. With
+    epilogue="residual", y holds the residual rows and receives the sums."""
     packed = lin.int4
     if packed is None:
         raise ValueError(f"{', '.join(lin.names)}: no INT4 weights")
@@ -99,6 +127,8 @@ def base_expand(lin: Lin, x: torch.Tensor, ws: Workspace, adp: torch.Tensor, y: 
     m = x.shape[0]
     if y.dtype != DT or tuple(y.shape) != (m, cols) or y.stride(1) != 1:
         raise ValueError(f"y must be bfloat16 ({m}, {cols}) with contiguous rows")
+    if epilogue == "residual":
+        _residual_rows(lin, x, y, epilogue, m)
     r = ws.routed(adp, lin.pool.shape[0], m)
     h = _lib.lib()
     flags = (0 if tiles is None else tiles.flags()) | eflag

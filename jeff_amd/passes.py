@@ -7,9 +7,11 @@ recorded input tensors and replays).
 The products of a pass share one routing launch only inside the capture that recorded it (Workspace.routed), so a
 replay routes the adapter ids and sequence lengths it finds in the recorded tensors, whatever the warm-up saw.
 `decoder_pass` is the layer body of the configurations' decoder (per layer: qkv, o with the residual add and
-RMSNorm, gate_up with SiLU(gate) * up in its output tile, down with the residual add and RMSNorm; the last token of
-each request gathered; the decision head), written with this package's calls; attention, which this build does not
-cover, is stood in for by the qkv product's first hidden-size columns."""
+RMSNorm, gate_up with SiLU(gate) * up, down with the residual add and RMSNorm; the last token of each request
+gathered; the decision head), written with this package's calls, either as the reference's sequence of products and
+element-wise launches (engine/fast_path.py:80-156) or with those element-wise steps in the products' output tiles
+(the residual add in o's and down's, SiLU(gate) * up in gate_up's), which give the same bits; attention, which this
+build does not cover, is stood in for by the qkv product's first hidden-size columns."""
 
 from __future__ import annotations
 
@@ -19,7 +21,7 @@ from typing import Any
 
 import torch
 
-from jeff_amd.epilogues import add_rms
+from jeff_amd.epilogues import add_rms, rms, silu_mul
 from jeff_amd.fast_path import Lin, Workspace
 from jeff_amd.int4_kernels import int4_product
 from jeff_amd.readout import readout_rows
@@ -62,15 +64,31 @@ class DecoderInputs:
 
 def decoder_pass(layers: Sequence[dict[str, Lin]], norms: Sequence[tuple[torch.Tensor, torch.Tensor]],
                  final_norm: torch.Tensor, ws: Workspace, inputs: DecoderInputs, tokens: int,
-                 readout_pool: torch.Tensor, temp_pool: torch.Tensor) -> Callable[[], torch.Tensor]:
+                 readout_pool: torch.Tensor, temp_pool: torch.Tensor, fused: bool = True) -> Callable[[], torch.Tensor]:
     """The body of one decoder pass over `layers` ({"qkv", "o", "gate_up", "down"} per layer, gate_up a gate and an
     up matrix of one width) with their RMSNorm weights (1 + weight, float32) before attention and before the MLP;
     returns a callable that runs the pass and returns the decision head's option probabilities (requests, options).
-    `tokens` is cu_seqlens' last value (the pass size the graph is recorded at)."""
+    `tokens` is cu_seqlens' last value (the pass size the graph is recorded at). fused: the residual adds and
+    SiLU(gate) * up in the products' output tiles (the residual stream a copy of inputs.x that the o and down
+    products update in place); else the reference's separate add_rms and silu_mul launches."""
     pool_rows = layers[0]["qkv"].pool.shape[0]
     hidden = layers[0]["o"].out
 
-    def body() -> torch.Tensor:
+    def body_fused() -> torch.Tensor:
+        ws.route(inputs.adp, pool_rows, tokens=tokens, cu_seqlens=inputs.cu_seqlens)
+        x = inputs.x.clone()  # the residual stream
+        for layer, (attn_norm, mlp_norm) in zip(layers, norms):
+            qkv = int4_product(layer["qkv"], rms(x, attn_norm), ws, inputs.adp)
+            # qkv's columns stand in for attention
+            int4_product(layer["o"], qkv[:, :hidden], ws, inputs.adp, epilogue="residual", residual=x)
+            act = int4_product(layer["gate_up"], rms(x, mlp_norm), ws, inputs.adp, epilogue="silu_mul")
+            int4_product(layer["down"], act, ws, inputs.adp, epilogue="residual", residual=x)
+        # the decision head reads each request's last token after the last residual add and the final norm
+        # (engine/batched_path.py:274-276)
+        hl = rms(x.index_select(0, inputs.ends), final_norm)
+        return readout_rows(hl, readout_pool, temp_pool, inputs.adp, inputs.counts)
+
+    def body_unfused() -> torch.Tensor:
         ws.route(inputs.adp, pool_rows, tokens=tokens, cu_seqlens=inputs.cu_seqlens)
         x = inputs.x
         _, h = add_rms(x, None, norms[0][0])
@@ -79,13 +97,11 @@ def decoder_pass(layers: Sequence[dict[str, Lin]], norms: Sequence[tuple[torch.T
             if i > 0:
                 x, h = add_rms(x, d, norms[i][0])
             qkv = int4_product(layer["qkv"], h, ws, inputs.adp)
-            d = int4_product(layer["o"], qkv[:, :hidden], ws, inputs.adp)  # qkv's columns stand in for attention
+            d = int4_product(layer["o"], qkv[:, :hidden], ws, inputs.adp)
             x, h = add_rms(x, d, mlp_norm)
-            act = int4_product(layer["gate_up"], h, ws, inputs.adp, epilogue="silu_mul")
+            act = silu_mul(int4_product(layer["gate_up"], h, ws, inputs.adp))
             d = int4_product(layer["down"], act, ws, inputs.adp)
-        # the decision head reads each request's last token after the last residual add and the final norm
-        # (engine/batched_path.py:274-276)
         _, hl = add_rms(x.index_select(0, inputs.ends), d.index_select(0, inputs.ends), final_norm)
         return readout_rows(hl, readout_pool, temp_pool, inputs.adp, inputs.counts)
 
-    return body
+    return body_fused if fused else body_unfused

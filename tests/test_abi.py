@@ -50,7 +50,9 @@ def test_header_constants_match_the_binding() -> None:
                         ("MLORA_FORCE_SHRINK_SEGMENT", _lib.FORCE_SHRINK_SEGMENT),
                         ("MLORA_FORCE_SHRINK_MFMA", _lib.FORCE_SHRINK_MFMA),
                         ("MLORA_FORCE_BASE_SPLIT", _lib.FORCE_BASE_SPLIT),
-                        ("MLORA_FORCE_BASE_NARROW", _lib.FORCE_BASE_NARROW)):
+                        ("MLORA_FORCE_BASE_NARROW", _lib.FORCE_BASE_NARROW),
+                        ("MLORA_EPILOGUE_SILU_MUL", _lib.EPILOGUE_SILU_MUL),
+                        ("MLORA_EPILOGUE_RESIDUAL", _lib.EPILOGUE_RESIDUAL)):
         assert const(name) == value
     assert re.search(r"#define MLORA_FORCE_RANGES\(s\) \(\(s\) << 8\)", text) and _lib.force_ranges(4) == 4 << 8
     assert ctypes.sizeof(_lib.Int4) == 8 * 3 + 4 * 4

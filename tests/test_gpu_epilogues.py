@@ -184,3 +184,84 @@ def test_silu_mul_epilogue_refusals() -> None:
         int4_product(case.lin, x, Workspace(8, 1, max_rank=16), adp, epilogue="silu_mul")
     with pytest.raises(ValueError, match="Unknown epilogue"):
         int4_product(case.lin, x, Workspace(8, 1, max_rank=16), adp, epilogue="gelu")
+
+
+RESIDUAL_CASES = {  # name: (tokens per request, requests, adapters, matrix widths, inputs, tiles, the kernel chosen)
+    "decode-narrow": (1, 160, 12, [512], 2048, None, "narrow"),
+    "decode-narrow-ranges": (1, 96, 12, [256], 1024, "narrow-4", "narrow"),
+    "decode-few-tokens": (1, 5, 12, [256], 512, None, "narrow"),  # 5 tokens: the narrow product, not the GEMV
+    "decode-split": (1, 600, 48, [256], 1024, None, "split"),
+    "prefill-fused": (64, 24, 12, [384, 128], 1024, None, "mfma"),
+    "prefill-small": (20, 6, 12, [256], 512, "mfma", "mfma"),  # 120 tokens: still the 256 x 256 kernel
+    "prefill-tail": (40, 26, 12, [128], 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
+}
+
+
+@pytest.mark.parametrize("name", list(RESIDUAL_CASES))
+def test_residual_add_in_the_product_tile_equals_add_rms_of_the_product(name: str) -> None:
+    """int4_product(..., epilogue="residual", residual=r) against the x that add_rms(r, product, w) gives on the plain
+    product (the same tiles), bit for bit, for every kernel family that takes it, with the last-token rows gathered;
+    and against the oracle's residual add."""
+    from jeff_amd import _lib
+    from jeff_amd.fast_path import Workspace
+    from jeff_amd.int4_kernels import int4_product
+    from jeff_amd.int4_tiles import Int4Tiles, int4_plan
+    from tests.gpu_cases import make_case
+
+    row_len, requests, adapters, widths, k, forced, kernel = RESIDUAL_CASES[name]
+    print(f"fused residual add {name}", flush=True)
+    ranks = {a: [(8, 16, 32)[(a + j) % 3] for j in range(len(widths))] for a in range(1, adapters + 1)}
+    case = make_case(widths, k, 128, True, ranks, [32] * len(widths), sum(widths) + k + 7)
+    lin = case.lin
+    tokens = row_len * requests
+    rng = np.random.default_rng(tokens + 1)
+    adp = torch.tensor(rng.integers(0, adapters + 1, requests).astype(np.int32), device="cuda")
+    x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
+    ws = Workspace(tokens, row_len, max_rank=lin.rank)
+    tiles = {None: None, "narrow-4": Int4Tiles("narrow", "segment", 4), "mfma": Int4Tiles("mfma", "mfma")}[forced]
+    flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_RESIDUAL
+    assert int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)[0] == kernel
+    plain = int4_product(lin, x, ws, adp, tiles=tiles)
+    r0 = (3 * torch.randn(tokens, lin.out, device="cuda")).to(torch.bfloat16)
+    res = r0.clone()
+    last = torch.zeros(requests, lin.out, dtype=torch.bfloat16, device="cuda")
+    got = int4_product(lin, x, ws, adp, tiles=tiles, last_out=last, epilogue="residual", residual=res)
+    assert got is res
+    xo, _ = add_rms(r0, plain, torch.ones(lin.out, device="cuda"))
+    assert torch.equal(res, xo)
+    assert torch.equal(last, res[row_len - 1::row_len])
+    xo_bits, _, _ = oracle_add_rms(bits(r0), bits(plain), np.ones(lin.out, np.float32))
+    assert np.array_equal(bits(res), xo_bits)
+
+
+def test_residual_epilogue_refusals() -> None:
+    from jeff_amd import _lib
+    from jeff_amd.fast_path import Workspace
+    from jeff_amd.int4_kernels import int4_product
+    from jeff_amd.int4_tiles import Int4Tiles
+    from tests.gpu_cases import make_case
+
+    case = make_case([256], 512, 128, True, {1: [8]}, [8], 5)
+    lin = case.lin
+    x = torch.randn(8, 512, device="cuda").to(torch.bfloat16)
+    adp = torch.ones(8, dtype=torch.int32, device="cuda")
+    ws = Workspace(8, 1, max_rank=16)
+    r = torch.zeros(8, 256, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="takes the residual rows"):
+        int4_product(lin, x, ws, adp, epilogue="residual")
+    with pytest.raises(ValueError, match="takes the residual rows"):
+        int4_product(lin, x, ws, adp, residual=r)
+    with pytest.raises(ValueError, match="residual must be a bfloat16"):
+        int4_product(lin, x, ws, adp, epilogue="residual", residual=r[:, :128])
+    flat = torch.zeros(8 * 512 + 8 * 256, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="must not overlap x"):  # rows of x and of the residual in one buffer
+        int4_product(lin, flat[:4096].view(8, 512), ws, adp, epilogue="residual",
+                     residual=flat[2048:4096].view(8, 256))
+    with pytest.raises(_lib.HipError, match="does not run"):  # the GEMV kernel has no epilogue
+        int4_product(lin, x, ws, adp, tiles=Int4Tiles("gemv", "segment"), epilogue="residual", residual=r)
+    h = _lib.lib()
+    rc = h.mlora_lora_add(lin.lora_abi(), ws.routed(adp, lin.pool.shape[0], 8), x.data_ptr(), x.stride(0), 512,
+                          r.data_ptr(), r.stride(0), 256, ws.mid.data_ptr(), ws.mid.numel() * 2,
+                          _lib.EPILOGUE_RESIDUAL, torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.EUNSUPPORTED
+    assert not r.any()  # nothing ran

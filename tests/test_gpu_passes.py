@@ -1,9 +1,10 @@
 """A whole decoder pass recorded as one HIP graph (jeff_amd.passes) and replayed for new batches (needs a gfx950 GPU;
-marked gpu): two layers of qkv, o + residual add + RMSNorm, gate_up with SiLU(gate) * up in its output tile, down +
-residual add + RMSNorm, the last-token gather and the decision head, with ragged requests over a pool of adapters of
-mixed ranks. Each replay, after new adapter ids, sequence lengths, inputs and option counts are copied into the
-recorded tensors (engine/batched_path.py:589-603), must give the bits an eager run of the same body gives; every
-kernel it runs is checked against the oracle in its own tests."""
+marked gpu): two layers of qkv, o + residual add + RMSNorm, gate_up with SiLU(gate) * up, down + residual add +
+RMSNorm, the last-token gather and the decision head, with ragged requests over a pool of adapters of mixed ranks,
+the residual adds and the gated activation in the products' output tiles. Each replay, after new adapter ids,
+sequence lengths, inputs and option counts are copied into the recorded tensors (engine/batched_path.py:589-603),
+must give the bits an eager run of the same body gives, and so must the reference's sequence of separate launches
+(add_rms, silu_mul); every kernel it runs is checked against the oracle in its own tests."""
 
 from __future__ import annotations
 
@@ -77,6 +78,7 @@ def test_a_recorded_decoder_pass_replays_new_batches_as_an_eager_run() -> None:
                            counts=torch.tensor(counts.astype(np.int32), device="cuda"))
     ws = Workspace(tokens, 1, max_rank=max(lin.rank for lin in lins), max_requests=requests)
     body = decoder_pass(layers, norms, final_norm, ws, inputs, tokens, readout_pool, temp_pool)
+    unfused = decoder_pass(layers, norms, final_norm, ws, inputs, tokens, readout_pool, temp_pool, fused=False)
     recorded = RecordedPass(body)
     seen = []
     for _ in range(3):
@@ -91,6 +93,7 @@ def test_a_recorded_decoder_pass_replays_new_batches_as_an_eager_run() -> None:
         eager = body()
         torch.cuda.synchronize()
         assert torch.equal(probs, eager)
+        assert torch.equal(unfused(), eager)  # the epilogues in the output tiles give the separate launches' bits
         assert bool(torch.isfinite(probs).all())
         sums = probs.sum(1)
         assert bool(((sums - 1).abs() < 1e-4).all())

@@ -135,6 +135,23 @@ def test_kernel_choice_rule() -> None:
         int4_tiles(100, 1024, 4)
 
 
+def test_kernel_choice_with_epilogues() -> None:
+    """The residual and gated epilogues never take the GEMV kernel (it has no epilogue): few tokens run the narrow
+    product; forcing the GEMV, or both epilogues at once, is refused."""
+    from jeff_amd import _lib
+    from jeff_amd.int4_tiles import int4_plan
+
+    assert int4_plan(2048, 2048, 5)[0] == "gemv"
+    assert int4_plan(2048, 2048, 5, flags=_lib.EPILOGUE_RESIDUAL)[0] == "narrow"
+    assert int4_plan(12288, 2048, 5, flags=_lib.EPILOGUE_SILU_MUL)[0] == "narrow"
+    assert int4_plan(2048, 6144, 159488, 512, 129, 32, flags=_lib.EPILOGUE_RESIDUAL)[0] == "mfma"
+    assert int4_plan(2048, 6144, 4096, 4096, 1025, 64, flags=_lib.EPILOGUE_RESIDUAL)[0] == "split"
+    with pytest.raises(ValueError, match="does not run"):
+        int4_plan(2048, 2048, 5, flags=_lib.EPILOGUE_RESIDUAL | _lib.FORCE_BASE_GEMV)
+    with pytest.raises(ValueError, match="invalid|argument"):
+        int4_plan(12288, 2048, 64, flags=_lib.EPILOGUE_RESIDUAL | _lib.EPILOGUE_SILU_MUL)
+
+
 GROUPS = ("layers.0.mlp.gate_proj, layers.0.mlp.up_proj", "layers.0.mlp.down_proj")
 
 
