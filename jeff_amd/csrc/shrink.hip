@@ -5,9 +5,9 @@
 //  - shrink_seg: few tokens per adapter (decode). One workgroup per (segment, 32-rank block) streams those 32 rows
 //    of A once into MFMA operands, the segment's rows as the other operand; its waves split the inputs and add their
 //    sums in a fixed order. Memory-bound on A.
-//  - shrink_mfma: long segments (prefill). Workgroups per 32 sorted positions; their waves split the inputs, stream
-//    the x rows through per-wave LDS rings two chunks ahead and A into registers one chunk ahead, and add their
-//    partial sums in a fixed order.
+//  - shrink_tile: long segments (prefill). Workgroups per 128 sorted positions, 4 waves of 32 rows; the x rows and
+//    the adapter's A rows stream through LDS rings two steps ahead, A shared by the waves; each wave sums its rows
+//    over all the inputs in order.
 #include "shrink_seg.h"
 #include "tile_common.h"
 
@@ -15,168 +15,135 @@ namespace {
 
 using namespace mlora;
 
-constexpr int kSRows = 32;    // sorted rows per workgroup
-constexpr int kSWaves = 4;    // waves per workgroup, each a contiguous share of the inputs (two workgroups per CU)
 constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
 
-// Per-wave rings of three x chunks (32 rows x 64 inputs each), distinct arrays so the slot is known at compile time.
-__shared__ __attribute__((aligned(16))) uint16_t s_ring0[kSWaves * kSRows * kSChunk];
-__shared__ __attribute__((aligned(16))) uint16_t s_ring1[kSWaves * kSRows * kSChunk];
-__shared__ __attribute__((aligned(16))) uint16_t s_ring2[kSWaves * kSRows * kSChunk];
+__device__ __forceinline__ void drain_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Long segments (prefill): two workgroups per 32 sorted rows, (block, 0) for the block's first adapter segment and
-// (block, 1) for the rest (none, unless the block crosses a segment boundary), so a crossing block does not take
-// twice as long as the others. A workgroup's 4 waves split the input dimension into chunks of 64. A wave streams its
-// chunks of the 32 x rows (gathered through the sorted order) into its own three-slot LDS ring with loads that cover
-// whole 128-byte rows, two chunks ahead, and loads the matching A operands into registers one chunk ahead; one
-// 32x32x16 MFMA per 32-rank block and 16 inputs, A as the first operand so a lane's accumulators hold four
-// consecutive ranks of one token. The four partial sums are added in wave order in LDS and rounded once. Rows
-// outside the segment read zero x operands.
-// KB: 32-rank blocks per pass (1, 2 or 3, chosen by the host from the group's capacities: all of an adapter's blocks
-// in one pass when there are one or three, so no block slot is a masked re-read)
-template <int KB>
-__global__ __launch_bounds__(kSWaves * 64) void shrink_mfma_kernel(mlora_lora_t L, mlora_route_t r,
-                                                                  const uint16_t* __restrict__ x, int64_t x_stride,
-                                                                  int32_t k, uint16_t* __restrict__ mid) {
-  constexpr int kSLoads = 4 + 4 * KB;  // memory instructions per chunk and lane: x rows to LDS, then A
+template <int RB>
+__global__ __launch_bounds__(256) void shrink_tile_kernel(mlora_lora_t L, mlora_route_t r,
+                                                          const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
+                                                          uint16_t* __restrict__ mid) {
+  constexpr int kRows = 128;
+  constexpr int kLoads = 4 + RB;  // memory instructions per lane and step: x rows, then A rows
+  static_assert(RB >= 1 && RB <= 4, "at most 4 blocks of A per pass");
+  // rings of three x buffers (128 rows x 64 inputs) and three A buffers (RB blocks of 32 stacked ranks x 64 inputs),
+  // distinct arrays so each slot is known at compile time (sized by RB: one or two blocks leave room for a second
+  // workgroup on the CU)
+  __shared__ __attribute__((aligned(16))) uint16_t t_x0[kRows * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_x1[kRows * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_x2[kRows * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_a0[RB * 32 * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_a1[RB * 32 * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_a2[RB * 32 * kSChunk];
   const int64_t T = r.tokens;
-  const int64_t p0 = (int64_t)blockIdx.x * kSRows;
+  const int64_t p0 = (int64_t)blockIdx.x * kRows;
   if (p0 >= T) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t prow = p0 + (lane & 31);
-  const int nch = k / kSChunk;
-  const int c0 = (wave * nch) / kSWaves, c1 = ((wave + 1) * nch) / kSWaves;  // this wave's chunks
-  // x staging: instruction i fills rows 8 i .. 8 i + 7 of the wave's ring slot; lane l writes 16-byte slot l & 7 of
-  // row 8 i + (l >> 3), which holds logical chunk swz_slot(row, l & 7)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int s_first = r.seg_of[p0], s_last = r.seg_of[min(p0 + kRows, T) - 1];
+  const int s_lo = blockIdx.y == 0 ? s_first : s_first + 1, s_hi = blockIdx.y == 0 ? s_first : s_last;
+  if (s_lo > s_hi) return;
+  // x staging: instruction i of wave w fills rows 8 (4 i + w) .. +7; lane l writes 16-byte slot l & 7 of row
+  // +(l >> 3), which holds logical chunk swz_slot(row, l & 7). Rows past the tokens read the tile's first row.
   const uint16_t* xsrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 8 * i + (lane >> 3);
+    const int row = 8 * (4 * i + wave) + (lane >> 3);
     const int64_t p = p0 + row;
     xsrc[i] = x + (int64_t)r.tok_perm[p < T ? p : p0] * x_stride + 8 * swz_slot(row, lane & 7);
   }
-  uint16_t* const ring0 = s_ring0 + wave * kSRows * kSChunk;
-  uint16_t* const ring1 = s_ring1 + wave * kSRows * kSChunk;
-  uint16_t* const ring2 = s_ring2 + wave * kSRows * kSChunk;
-  const int orow = lane & 31;  // the operand row of this lane
-  const int s_first = r.seg_of[p0], s_last = r.seg_of[min(p0 + kSRows, T) - 1];
-  // workgroup (block, 0) takes the block's first segment, (block, 1) the others, so a block that crosses a segment
-  // boundary is not twice as long as the rest
-  const int s_lo = blockIdx.y == 0 ? s_first : s_first + 1, s_hi = blockIdx.y == 0 ? s_first : s_last;
+  const int nk = k / kSChunk;
+  const int R = L.rank_cap, nblk = (R + 31) / 32;
+  const int orow = wave * 32 + (lane & 31);  // the lane's x operand row (and token of its accumulators)
+  const int64_t prow = p0 + orow;
   for (int s = s_lo; s <= s_hi; ++s) {
     const int a = r.seg_adapter[s];
     if (a == 0) continue;  // the base row: no first factor is read
     const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
-    const bool rin = prow >= sb && prow < se;
-    int rk[MLORA_MAX_MATS];
-    int nblk = 0;
-    for (int j = 0; j < L.n_mats; ++j) {
-      rk[j] = live_rank(L, a, j);
-      nblk += (rk[j] + 31) >> 5;
-    }
-    const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a + 8 * (lane >> 5);
-    for (int b0 = 0; b0 < nblk; b0 += KB) {
-      const uint16_t* asrc[KB];
-      bool aok[KB];
+    const uint16_t* Abase = L.pool + (int64_t)a * L.pool_stride + L.off_a;
+    const int passes = (nblk + RB - 1) / RB;
+    for (int pass = 0; pass < passes; ++pass) {
+      const int b0 = pass * RB;
+      // A staging: instruction i of wave w fills stacked rows 32 b0 + 8 (4 i + w) .. +7 (rows past R re-read row
+      // R - 1, never written out)
+      // (a fixed-size array: captured by the lambdas below, an array sized by RB kept the compiler from emitting the
+      // kernel's host-side launch stubs)
+      const uint16_t* asrc[4];
 #pragma unroll
-      for (int bi = 0; bi < KB; ++bi) {
-        int j = 0, kb = 0;
-        rank_block(rk, L.n_mats, min(b0 + bi, nblk - 1), j, kb);
-        const int n = kb * 32 + (lane & 31);
-        aok[bi] = b0 + bi < nblk && n < rk[j];
-        asrc[bi] = Abase + (int64_t)(rank_offset(L, j) + (aok[bi] ? n : 0)) * k;
+      for (int i = 0; i < 4; ++i) {
+        const int row = 8 * (4 * i + wave) + (lane >> 3);
+        asrc[i] = Abase + (int64_t)min(32 * b0 + row, R - 1) * k + 8 * swz_slot(row, lane & 7);
       }
-      f32x16_t acc[KB];
+      // a step's loads into ring slot (xs, as); past the last step they re-read it (the same number of loads in
+      // flight at every wait)
+      auto issue = [&](uint16_t* xs, uint16_t* as, int c) __attribute__((always_inline)) {
+        const int kc = min(c, nk - 1) * kSChunk;
 #pragma unroll
-      for (int bi = 0; bi < KB; ++bi) acc[bi] = f32x16_t{};
-      // rows outside the segment and rank rows past the live rank multiply as zeros (bit masks, not branches)
-      const uint32_t xmask = rin ? 0xFFFFFFFFu : 0u;
-      uint32_t amask[KB];
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_global_load_lds(xsrc[i] + kc, (lds_void*)(xs + 8 * (4 * i + wave) * kSChunk), 16, 0, 0);
 #pragma unroll
-      for (int bi = 0; bi < KB; ++bi) amask[bi] = aok[bi] ? 0xFFFFFFFFu : 0u;
-      if (c1 > c0) {
-        uint4 aq0[4][KB], aq1[4][KB];
-        // a chunk's x rows into a ring slot and its A operands into registers; every load is unconditional (chunks
-        // past the wave's range re-read its last one), so the counts the waits rely on hold on every path
-        auto issue_x = [&](uint16_t* slot, int c) {
-          const int kc = min(c, c1 - 1) * kSChunk;
+        for (int i = 0; i < RB; ++i)
+          __builtin_amdgcn_global_load_lds(asrc[i] + kc, (lds_void*)(as + 8 * (4 * i + wave) * kSChunk), 16, 0, 0);
+      };
+      f32x16_t acc[RB];
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(xsrc[i] + kc, (lds_void*)(slot + i * 8 * kSChunk), 16, 0, 0);
-        };
-        auto issue_a = [&](uint4 (&aq)[4][KB], int c) {
-          const int kc = min(c, c1 - 1) * kSChunk;
+      for (int bi = 0; bi < RB; ++bi) acc[bi] = f32x16_t{};
+      auto compute = [&](const uint16_t* xs, const uint16_t* as) __attribute__((always_inline)) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
+          const int c = 2 * t + (lane >> 5);
+          const uint4 xv = *reinterpret_cast<const uint4*>(&xs[swz(orow, c)]);
 #pragma unroll
-            for (int bi = 0; bi < KB; ++bi)
-              aq[t][bi] = *reinterpret_cast<const uint4*>(asrc[bi] + kc + 16 * t);
-        };
-        auto compute = [&](const uint16_t* slot, const uint4 (&aq)[4][KB]) {
-          uint4 xo[4];  // the chunk's four x operands, read before the first MFMA
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            xo[t] = *reinterpret_cast<const uint4*>(&slot[swz(orow, 2 * t + (lane >> 5))]);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint4 xv = make_uint4(xo[t].x & xmask, xo[t].y & xmask, xo[t].z & xmask, xo[t].w & xmask);
-#pragma unroll
-            for (int bi = 0; bi < KB; ++bi) {
-              const uint4 av = aq[t][bi];
-              acc[bi] = mfma32(make_uint4(av.x & amask[bi], av.y & amask[bi], av.z & amask[bi], av.w & amask[bi]), xv,
-                               acc[bi]);
-            }
+          for (int bi = 0; bi < RB; ++bi) {
+            const uint4 av = *reinterpret_cast<const uint4*>(&as[swz(bi * 32 + (lane & 31), c)]);
+            acc[bi] = mfma32(av, xv, acc[bi]);
           }
-        };
-        // x rows two chunks ahead (three LDS slots), A operands one chunk ahead (two register sets): the loads are
-        // issued x(c + 2), A(c + 1) before chunk c is used, so chunk c has landed when the 4 + 8 loads issued after
-        // A(c) are the only ones outstanding
-        auto sub = [&](uint16_t* xf, uint4 (&an)[4][KB], const uint16_t* xs, const uint4 (&ac)[4][KB],
-                       int c) {
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // the previous chunk's LDS reads are done before its slot is refilled
-          issue_x(xf, c + 2);
-          issue_a(an, c + 1);
-          MLORA_WAIT_VM(kSLoads);  // chunk c (x rows and A) has landed
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-          compute(xs, ac);
-        };
-        issue_x(ring0, c0);
-        issue_x(ring1, c0 + 1);
-        issue_a(aq0, c0);
-        for (int c = c0; c < c1; c += 6) {
-          sub(ring2, aq1, ring0, aq0, c);
-          if (c + 1 >= c1) break;
-          sub(ring0, aq0, ring1, aq1, c + 1);
-          if (c + 2 >= c1) break;
-          sub(ring1, aq1, ring2, aq0, c + 2);
-          if (c + 3 >= c1) break;
-          sub(ring2, aq0, ring0, aq1, c + 3);
-          if (c + 4 >= c1) break;
-          sub(ring0, aq1, ring1, aq0, c + 4);
-          if (c + 5 >= c1) break;
-          sub(ring1, aq0, ring2, aq1, c + 5);
         }
-        MLORA_WAIT_VM(0);
+      };
+      // Step i: its loads landed (the wave's own: at most the next step's are in flight), the barrier (every wave's
+      // have, and every wave is done reading step i - 1's slot), then step i + 2's loads into that slot, then the
+      // MFMAs of step i.
+      __syncthreads();  // the previous pass (or segment) is done reading the rings
+      issue(t_x0, t_a0, 0);
+      issue(t_x1, t_a1, 1);
+      auto step = [&](const uint16_t* xs, const uint16_t* as, uint16_t* xf, uint16_t* af, int i)
+          __attribute__((always_inline)) {
+        MLORA_WAIT_VM(kLoads);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        issue(xf, af, i + 2);
+        compute(xs, as);
+        drain_lds();  // this step's LDS reads are done before the next barrier
+      };
+      for (int i = 0; i < nk; i += 3) {
+        step(t_x0, t_a0, t_x2, t_a2, i);
+        if (i + 1 >= nk) break;
+        step(t_x1, t_a1, t_x0, t_a0, i + 1);
+        if (i + 2 >= nk) break;
+        step(t_x2, t_a2, t_x1, t_a1, i + 2);
       }
-      // the waves' sums in wave order, one 32-rank block at a time through LDS (the rings are free)
-      float* red = reinterpret_cast<float*>(s_ring0);  // [wave][register][lane]
+      MLORA_WAIT_VM(0);
+      // lane l holds, for token p0 + orow and block bi, stacked ranks 32 (b0 + bi) + 8 g + 4 (l >> 5) + e
+      if (prow >= sb && prow < se && prow < T) {
+        uint16_t* mrow = mid + prow * R;
 #pragma unroll
-      for (int bi = 0; bi < KB; ++bi) {
-        __syncthreads();  // every wave is done with the rings (and the previous block's sums)
+        for (int bi = 0; bi < RB; ++bi) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc[bi][i];
-        __syncthreads();
-        if (b0 + bi < nblk) {
-          int j = 0, kb = 0;
-          rank_block(rk, L.n_mats, b0 + bi, j, kb);
-          for (int e = tid; e < 16 * kWave; e += kSWaves * kWave) {
-            const int i = e / kWave, ln = e % kWave;
-            float sum = red[i * kWave + ln];
-#pragma unroll
-            for (int w = 1; w < kSWaves; ++w) sum += red[(w * 16 + i) * kWave + ln];
-            const int n = kb * 32 + (i >> 2) * 8 + (ln >> 5) * 4 + (i & 3);
-            const int64_t p = p0 + (ln & 31);
-            if (n < rk[j] && p >= sb && p < se) mid[p * L.rank_cap + rank_offset(L, j) + n] = f32_to_bf16(sum);
+          for (int g = 0; g < 4; ++g) {
+            const int n0 = 32 * (b0 + bi) + 8 * g + 4 * (lane >> 5);
+            if (n0 >= R) continue;
+            // the matrix holding rank n0 (capacities are multiples of 8, so the four ranks n0..n0+3 share it)
+            int j = 0, rho = 0;
+            while (j + 1 < L.n_mats && n0 >= rho + L.cap[j]) rho += L.cap[j++];
+            const int live = live_rank(L, a, j) - (n0 - rho);  // ranks n0.. of matrix j below its live rank
+            const uint32_t lo = pack_bf16x2(acc[bi][4 * g], acc[bi][4 * g + 1]);
+            const uint32_t hi = pack_bf16x2(acc[bi][4 * g + 2], acc[bi][4 * g + 3]);
+            if (live >= 4) {
+              *reinterpret_cast<uint2*>(mrow + n0) = make_uint2(lo, hi);
+            } else {
+              const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+              for (int e = 0; e < live; ++e) mrow[n0 + e] = h[e];
+            }
           }
         }
       }
@@ -199,17 +166,19 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
                     uint16_t* mid, bool mfma, hipStream_t stream) {
   if (r.tokens == 0 || r.max_segs == 0) return MLORA_OK;
   if (mfma) {
-    const int64_t blocks = (r.tokens + kSRows - 1) / kSRows;
-    // blocks per pass: all of an adapter's blocks when that is one or three (every capacity a multiple of 32), else 2
-    int cap_blocks = 0;
-    for (int j = 0; j < L.n_mats; ++j) cap_blocks += (L.cap[j] + 31) / 32;
-    const dim3 grid((unsigned)blocks, 2);
-    if (cap_blocks == 1)
-      hipLaunchKernelGGL(shrink_mfma_kernel<1>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
-    else if (cap_blocks == 3)
-      hipLaunchKernelGGL(shrink_mfma_kernel<3>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
+    // 32-rank blocks of the stacked capacity, in passes of at most 4 (as even as the count allows)
+    const int nblk = (L.rank_cap + 31) / 32;
+    if (nblk == 0) return MLORA_OK;
+    const int passes = (nblk + 3) / 4, rb = (nblk + passes - 1) / passes;
+    const dim3 grid((unsigned)((r.tokens + 127) / 128), 2);
+    if (rb == 1)
+      hipLaunchKernelGGL(shrink_tile_kernel<1>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+    else if (rb == 2)
+      hipLaunchKernelGGL(shrink_tile_kernel<2>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+    else if (rb == 3)
+      hipLaunchKernelGGL(shrink_tile_kernel<3>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
     else
-      hipLaunchKernelGGL(shrink_mfma_kernel<2>, grid, dim3(kSWaves * 64), 0, stream, L, r, x, x_stride, k, mid);
+      hipLaunchKernelGGL(shrink_tile_kernel<4>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
   } else {
     int max_blocks = 0;  // 32-rank blocks of an adapter using every matrix's capacity
     for (int j = 0; j < L.n_mats; ++j) max_blocks += (L.cap[j] + 31) / 32;
