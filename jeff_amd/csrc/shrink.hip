@@ -8,6 +8,8 @@
 //  - shrink_tile: long segments (prefill). Workgroups per 128 sorted positions, 4 waves of 32 rows; the x rows and
 //    the adapter's A rows stream through LDS rings two steps ahead, A shared by the waves; each wave sums its rows
 //    over all the inputs in order.
+#include <type_traits>
+
 #include "shrink_seg.h"
 #include "tile_common.h"
 
@@ -19,22 +21,43 @@ constexpr int kSChunk = 64;   // inputs per staged chunk (128-byte rows)
 
 __device__ __forceinline__ void drain_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-template <int RB>
+template <int RB, int D>
 __global__ __launch_bounds__(256) void shrink_tile_kernel(mlora_lora_t L, mlora_route_t r,
                                                           const uint16_t* __restrict__ x, int64_t x_stride, int32_t k,
                                                           uint16_t* __restrict__ mid) {
   constexpr int kRows = 128;
   constexpr int kLoads = 4 + RB;  // memory instructions per lane and step: x rows, then A rows
   static_assert(RB >= 1 && RB <= 4, "at most 4 blocks of A per pass");
-  // rings of three x buffers (128 rows x 64 inputs) and three A buffers (RB blocks of 32 stacked ranks x 64 inputs),
-  // distinct arrays so each slot is known at compile time (sized by RB: one or two blocks leave room for a second
-  // workgroup on the CU)
+  static_assert(D >= 3 && D <= 5, "rings of 3 to 5 slots");
+  // rings of D x buffers (128 rows x 64 inputs) and D A buffers (RB blocks of 32 stacked ranks x 64 inputs), distinct
+  // arrays so each slot is known at compile time; only the first D of each are used (and allocated). The host picks
+  // D for the LDS a workgroup may take: two per CU, or one with more steps in flight.
   __shared__ __attribute__((aligned(16))) uint16_t t_x0[kRows * kSChunk];
   __shared__ __attribute__((aligned(16))) uint16_t t_x1[kRows * kSChunk];
   __shared__ __attribute__((aligned(16))) uint16_t t_x2[kRows * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_x3[kRows * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_x4[kRows * kSChunk];
   __shared__ __attribute__((aligned(16))) uint16_t t_a0[RB * 32 * kSChunk];
   __shared__ __attribute__((aligned(16))) uint16_t t_a1[RB * 32 * kSChunk];
   __shared__ __attribute__((aligned(16))) uint16_t t_a2[RB * 32 * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_a3[RB * 32 * kSChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t t_a4[RB * 32 * kSChunk];
+  auto xslot = [&](auto slot) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot)::value % D;
+    if constexpr (S == 0) return t_x0;
+    else if constexpr (S == 1) return t_x1;
+    else if constexpr (S == 2) return t_x2;
+    else if constexpr (S == 3) return t_x3;
+    else return t_x4;
+  };
+  auto aslot = [&](auto slot) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot)::value % D;
+    if constexpr (S == 0) return t_a0;
+    else if constexpr (S == 1) return t_a1;
+    else if constexpr (S == 2) return t_a2;
+    else if constexpr (S == 3) return t_a3;
+    else return t_a4;
+  };
   const int64_t T = r.tokens;
   const int64_t p0 = (int64_t)blockIdx.x * kRows;
   if (p0 >= T) return;
@@ -100,27 +123,43 @@ __global__ __launch_bounds__(256) void shrink_tile_kernel(mlora_lora_t L, mlora_
           }
         }
       };
-      // Step i: its loads landed (the wave's own: at most the next step's are in flight), the barrier (every wave's
-      // have, and every wave is done reading step i - 1's slot), then step i + 2's loads into that slot, then the
-      // MFMAs of step i.
+      // Step i reads slot i % D. Its loads landed (the wave's own: at most those of the D - 2 steps after it are in
+      // flight), then the barrier (every wave's have, and every wave is done reading step i - 1's slot), then step
+      // i + D - 1's loads into that slot, then the MFMAs of step i.
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      using I4 = std::integral_constant<int, 4>;
       __syncthreads();  // the previous pass (or segment) is done reading the rings
-      issue(t_x0, t_a0, 0);
-      issue(t_x1, t_a1, 1);
-      auto step = [&](const uint16_t* xs, const uint16_t* as, uint16_t* xf, uint16_t* af, int i)
-          __attribute__((always_inline)) {
-        MLORA_WAIT_VM(kLoads);
+      issue(xslot(I0{}), aslot(I0{}), 0);
+      issue(xslot(I1{}), aslot(I1{}), 1);
+      if constexpr (D > 3) issue(xslot(I2{}), aslot(I2{}), 2);
+      if constexpr (D > 4) issue(xslot(I3{}), aslot(I3{}), 3);
+      auto step = [&](auto slot, int i) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot)::value;
+        MLORA_WAIT_VM((D - 2) * kLoads);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        issue(xf, af, i + 2);
-        compute(xs, as);
+        issue(xslot(std::integral_constant<int, S + D - 1>{}), aslot(std::integral_constant<int, S + D - 1>{}),
+              i + D - 1);
+        compute(xslot(slot), aslot(slot));
         drain_lds();  // this step's LDS reads are done before the next barrier
       };
-      for (int i = 0; i < nk; i += 3) {
-        step(t_x0, t_a0, t_x2, t_a2, i);
+      for (int i = 0; i < nk; i += D) {
+        step(I0{}, i);
         if (i + 1 >= nk) break;
-        step(t_x1, t_a1, t_x0, t_a0, i + 1);
+        step(I1{}, i + 1);
         if (i + 2 >= nk) break;
-        step(t_x2, t_a2, t_x1, t_a1, i + 2);
+        step(I2{}, i + 2);
+        if constexpr (D > 3) {
+          if (i + 3 >= nk) break;
+          step(I3{}, i + 3);
+        }
+        if constexpr (D > 4) {
+          if (i + 4 >= nk) break;
+          step(I4{}, i + 4);
+        }
       }
       MLORA_WAIT_VM(0);
       // lane l holds, for token p0 + orow and block bi, stacked ranks 32 (b0 + bi) + 8 g + 4 (l >> 5) + e
@@ -171,14 +210,16 @@ int launch_shrink(const mlora_lora_t& L, const mlora_route_t& r, const uint16_t*
     if (nblk == 0) return MLORA_OK;
     const int passes = (nblk + 3) / 4, rb = (nblk + passes - 1) / passes;
     const dim3 grid((unsigned)((r.tokens + 127) / 128), 2);
+    // ring slots: 20 KB a slot at one block (4 slots, two workgroups per CU), 24 KB at two (3 slots, two per CU),
+    // 28 and 32 KB at three and four (5 and 4 slots, one per CU)
     if (rb == 1)
-      hipLaunchKernelGGL(shrink_tile_kernel<1>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+      hipLaunchKernelGGL((shrink_tile_kernel<1, 4>), grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
     else if (rb == 2)
-      hipLaunchKernelGGL(shrink_tile_kernel<2>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+      hipLaunchKernelGGL((shrink_tile_kernel<2, 3>), grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
     else if (rb == 3)
-      hipLaunchKernelGGL(shrink_tile_kernel<3>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+      hipLaunchKernelGGL((shrink_tile_kernel<3, 5>), grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
     else
-      hipLaunchKernelGGL(shrink_tile_kernel<4>, grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
+      hipLaunchKernelGGL((shrink_tile_kernel<4, 4>), grid, dim3(256), 0, stream, L, r, x, x_stride, k, mid);
   } else {
     int max_blocks = 0;  // 32-rank blocks of an adapter using every matrix's capacity
     for (int j = 0; j < L.n_mats; ++j) max_blocks += (L.cap[j] + 31) / 32;
