@@ -294,6 +294,41 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
                                                 "and the norm; the fused product reads x and writes x + d in its "
                                                 "output tile, rms reads x + d and writes the norm"}
 
+    if name == "decode-28l":
+        # the few-token GEMV (at most 8 tokens: base_gemv_kernel) at this workload's gate_up shape: its first 8
+        # requests (one token each) and their adapters, the plain product, timed as the dominant kernel is; HBM-bound
+        # on the weights
+        gl = w.layers[0]["gate_up"]
+        t8 = 8
+        x8 = xs[(0, "gate_up")][:t8]
+        adp8 = w.adp[:t8].contiguous()
+        cu8 = torch.arange(t8 + 1, dtype=torch.int32, device=dev)
+        ws8 = Workspace(t8, 1, max_rank=gl.rank, max_requests=t8)
+        y8 = torch.empty(t8, gl.out, dtype=DT, device=dev)
+        base8 = int4_plan(gl.int4.columns, gl.k, t8, t8, pool_rows, gl.rank, gl.out)[0]
+        ws8.route(adp8, pool_rows, tokens=t8, cu_seqlens=cu8)
+        shrink(gl, x8, ws8, adp8)
+
+        def gemv_then(k: int):
+            def fn() -> None:
+                ws8.route(adp8, pool_rows, tokens=t8, cu_seqlens=cu8)
+                for _ in range(k):
+                    base_expand(gl, x8, ws8, adp8, y8)
+            return fn
+
+        g_reps = 100
+        ggraph, grgraph = capture(gemv_then(g_reps), 1), capture(gemv_then(0), 1)
+        gms = (replay_ms(ggraph, stream, 1) - replay_ms(grgraph, stream, 1)) / g_reps
+        del ggraph, grgraph
+        ids8 = sorted({int(a) for a in adp8.cpu().tolist()} - {0})
+        gbytes = float(gl.int4.nbytes()) + 2.0 * t8 * (gl.k + gl.out)
+        gbytes += sum(2.0 * min(w.adapter_ranks[a], c) * n for a in ids8 for n, c in zip(gl.sizes, gl.caps))
+        result["gemv"] = {"kernel": f"{base8} (base_gemv_kernel<true>: INT4 base + fused LoRA expand)",
+                          "group": "layer0.gate_up", "tokens": t8, "adapters": len(ids8), "ms": gms,
+                          "bytes": gbytes, "achieved_gb_s": gbytes / (gms / 1e3) / 1e9,
+                          "hbm_frac": gbytes / (gms / 1e3) / PEAK_HBM}
+        del x8, ws8, y8
+
     if w.readout is not None:  # the decision head alone: its two launches, timed as the dominant kernel is
         r = w.readout
         hreps = 50

@@ -7,9 +7,10 @@
 //  - base_mfma: tiles of 128 sorted tokens x 128 columns, 4 waves of 64 x 64, 32x32x16 bf16 MFMA. Each K step of 64
 //    stages x (gathered through the sorted order) and the dequantised weights through LDS; the next step's words and
 //    activations are fetched into registers while the MFMAs run.
-//  - base_gemv: at most 8 tokens (decode of a few rows). 16 input slices x 64 columns per workgroup, each weight
-//    word dequantised once and dotted with every token (v_dot2_f32_bf16), slices summed in a fixed order in LDS.
-#include "mlora_common.h"
+//  - base_gemv: at most 8 tokens (decode of a few rows). 64 input slices x 16 columns per workgroup, x staged in LDS
+//    by chunks of 2048 inputs, each weight word dequantised once and dotted with every token (v_dot2_f32_bf16),
+//    slices summed in a fixed order in LDS.
+#include "tile_common.h"
 
 namespace {
 
@@ -184,84 +185,141 @@ __global__ __launch_bounds__(256) void base_mfma_kernel(mlora_int4_t w, mlora_lo
     }
 }
 
-constexpr int kGvCols = 64, kGvSlices = 16;
+constexpr int kGvCols = 16, kGvSlices = 64;  // columns per workgroup; input slices (4 columns x 64 slices = 256 threads)
 constexpr int kGvMaxTokens = 8;
+constexpr int kGvChunk = 2048;               // inputs of x staged in LDS at a time (8 rows x 4 KB)
+constexpr int kGvRows = kGvChunk / 8 / kGvSlices;  // word rows per thread and chunk
 constexpr int kBigTileTokens = 1024;  // from here on the 256 x 256 tiles of gemm256.hip fill the chip
 
+static_assert(kGvSlices * kGvMaxTokens * kGvCols * 4 <= kGvMaxTokens * kGvChunk * 2, "the sums reuse the x buffer");
+
+// At most 8 tokens. A workgroup takes 16 columns: thread (slice ks, column group cg) the 4 columns 4 cg .. +3 and the
+// word rows ks, ks + 64, ... of each 2048-input chunk. Per chunk, every thread first issues all its loads (the words
+// of its rows, their scales and zero points) and the workgroup stages the chunk of the 8 token rows of x in LDS
+// (loads that write LDS directly), then waits once; each word is dequantised once and dotted with every token
+// (v_dot2_f32_bf16). The 64 slices' sums are added in slice order through LDS (the x buffer's space), then each
+// output adds its LoRA term (eight ranks per 16-byte load) and is rounded once. Without the base (kBase = false) the
+// output adds the LoRA term to y in place (lora_add).
 template <bool kBase>
 __global__ __launch_bounds__(256) void base_gemv_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                        const uint16_t* __restrict__ x, int64_t x_stride,
                                                        uint16_t* __restrict__ y, int64_t y_stride,
                                                        uint16_t* __restrict__ last_out, int32_t n_out,
                                                        const uint16_t* __restrict__ mid) {
-  __shared__ float red[kGvSlices][kGvMaxTokens][kGvCols];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kGvMaxTokens * kGvChunk];
+  float* red = reinterpret_cast<float*>(xs);  // [slice][token][column], after the last chunk
   const int tid = threadIdx.x;
   const int n0 = blockIdx.x * kGvCols;
   const int T = (int)r.tokens;
   if constexpr (kBase) {
-    const int cg = tid & 15, ks = tid >> 4;  // 4 consecutive columns x one input slice per thread
-    const int c = n0 + cg * 4;               // columns is a multiple of 64: c + 3 < columns
-    float acc[kGvMaxTokens][4];
-    const uint16_t* xr[kGvMaxTokens];
+    const int cg = tid & 3, ks = tid >> 2;
+    const int c4 = n0 + cg * 4;  // columns is a multiple of 64: c4 + 3 < columns
+    const bool vec_sz = (reinterpret_cast<uintptr_t>(w.scales) & 7) == 0 &&
+                        (w.zeros == nullptr || (reinterpret_cast<uintptr_t>(w.zeros) & 3) == 0);
+    // x staging: instruction i of thread t moves 16 bytes: token row (256 i + t) / 256, 16-byte column (256 i + t)
+    // % 256 of the chunk (rows past the tokens read the last token's row; their sums are never written)
+    const uint16_t* xrow[kGvMaxTokens];
 #pragma unroll
-    for (int m = 0; m < kGvMaxTokens; ++m) {
-      xr[m] = x + (int64_t)r.tok_perm[min(m, T - 1)] * x_stride;
+    for (int m = 0; m < kGvMaxTokens; ++m) xrow[m] = x + (int64_t)r.tok_perm[min(m, T - 1)] * x_stride;
+    float acc[kGvMaxTokens][4];
+#pragma unroll
+    for (int m = 0; m < kGvMaxTokens; ++m)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[m][e] = 0.0f;
-    }
-    for (int wr = ks; wr < w.k / 8; wr += kGvSlices) {
-      const int64_t g = (int64_t)((8 * wr) / w.group) * w.columns + c;
-      const uint4 wv = *reinterpret_cast<const uint4*>(w.words + (int64_t)wr * w.columns + c);
-      const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint4 wq[4];
+    for (int k0 = 0; k0 < w.k; k0 += kGvChunk) {
+      const int kn = min(kGvChunk, w.k - k0);  // a multiple of 64
+      // the thread's word rows of this chunk, their scales and zero points
+      uint4 wv[kGvRows];
+      uint32_t sb[kGvRows][4], zb[kGvRows][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float s = bf16_to_f32(w.scales[g + e]);
-        const float z = w.zeros != nullptr ? (float)w.zeros[g + e] : 8.0f;
-        wq[e] = dequant_word(wd[e], s, z * s);
+      for (int i = 0; i < kGvRows; ++i) {
+        const int wr = (k0 + 8 * (ks + kGvSlices * i)) / 8;
+        const bool in = 8 * (ks + kGvSlices * i) < kn;
+        const int wrc = in ? wr : k0 / 8;  // rows past the chunk re-read its first (their products are not added)
+        const int64_t g = (int64_t)((8 * wrc) / w.group) * w.columns + c4;
+        wv[i] = *reinterpret_cast<const uint4*>(w.words + (int64_t)wrc * w.columns + c4);
+        if (vec_sz) {
+          const uint2 sv = *reinterpret_cast<const uint2*>(w.scales + g);
+          const uint32_t zv = w.zeros != nullptr ? *reinterpret_cast<const uint32_t*>(w.zeros + g) : 0x08080808u;
+          sb[i][0] = sv.x & 0xFFFF, sb[i][1] = sv.x >> 16, sb[i][2] = sv.y & 0xFFFF, sb[i][3] = sv.y >> 16;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) zb[i][e] = (zv >> (8 * e)) & 0xFF;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sb[i][e] = w.scales[g + e];
+            zb[i][e] = w.zeros != nullptr ? w.zeros[g + e] : 8;
+          }
+        }
       }
+      __syncthreads();  // the previous chunk's x reads are done
 #pragma unroll
-      for (int m = 0; m < kGvMaxTokens; ++m) {
-        if (m < T) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xr[m] + 8 * wr);
+      for (int i = 0; i < kGvMaxTokens; ++i) {
+        const int e = 256 * i + tid, m = e >> 8, c16 = e & 255;
+        if (8 * c16 < kn)
+          __builtin_amdgcn_global_load_lds(xrow[m] + k0 + 8 * c16, (lds_void*)(xs + m * kGvChunk + 8 * c16), 16, 0,
+                                           0);
+      }
+      MLORA_WAIT_VM(0);  // every load of this thread
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kGvRows; ++i) {
+        const int kk = 8 * (ks + kGvSlices * i);
+        if (kk >= kn) break;
+        const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        uint4 wq[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sc = bf16_to_f32(sb[i][e]);
+          wq[e] = dequant_word(wd[e], sc, (float)zb[i][e] * sc);
+        }
+#pragma unroll
+        for (int m = 0; m < kGvMaxTokens; ++m) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xs + m * kGvChunk + kk);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[m][e] = dot8(xv, wq[e], acc[m][e]);
         }
       }
     }
+    __syncthreads();  // the x buffer becomes the slices' sums
 #pragma unroll
     for (int m = 0; m < kGvMaxTokens; ++m)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[ks][m][cg * 4 + e] = acc[m][e];
+      for (int e = 0; e < 4; ++e) red[(ks * kGvMaxTokens + m) * kGvCols + cg * 4 + e] = acc[m][e];
     __syncthreads();
   }
-  const int nseg = *r.num_segs;
-  const int cl = tid & 63;
+  // output (token m, column c) of threads 0..127
+  const int m = tid / kGvCols, cl = tid % kGvCols;
   const int c = n0 + cl;
-  for (int m = tid >> 6; m < T; m += 4) {
-    if (c >= n_out) continue;
-    const int t = r.tok_perm[m];
-    float v;
-    if constexpr (kBase) {
-      v = 0.0f;
-#pragma unroll
-      for (int s = 0; s < kGvSlices; ++s) v += red[s][m][cl];
-    } else {
-      v = bf16_to_f32(y[(int64_t)t * y_stride + c]);
-    }
-    const int a = r.seg_adapter[segment_of(r.seg_start, nseg, m)];
-    if (a != 0) {
-      const int j = matrix_of(L, c);
-      const int rank = live_rank(L, a, j);
-      const uint16_t* mr = mid + (int64_t)m * L.rank_cap + rank_offset(L, j);
-      const uint16_t* br = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] +
-                             (int64_t)(c - col_offset(L, j)) * sb_stride(rank, L.cap[j]);
-      for (int q = 0; q < rank; ++q) v = __builtin_fmaf(bf16_to_f32(mr[q]), bf16_to_f32(br[q]), v);
-    }
-    const uint16_t o = f32_to_bf16(v);
-    y[(int64_t)t * y_stride + c] = o;
-    if (last_out != nullptr && r.last_of[m] >= 0) last_out[(int64_t)r.last_of[m] * n_out + c] = o;
+  if (tid >= kGvMaxTokens * kGvCols || m >= T || c >= n_out) return;
+  const int t = r.tok_perm[m];
+  float v;
+  if constexpr (kBase) {
+    v = 0.0f;
+    for (int s = 0; s < kGvSlices; ++s) v += red[(s * kGvMaxTokens + m) * kGvCols + cl];
+  } else {
+    v = bf16_to_f32(y[(int64_t)t * y_stride + c]);
   }
+  const int a = r.seg_adapter[r.seg_of[m]];
+  const int j = matrix_of(L, c);
+  const int rank = a != 0 ? live_rank(L, a, j) : 0;
+  if (rank > 0) {
+    const uint16_t* mr = mid + (int64_t)m * L.rank_cap + rank_offset(L, j);
+    const uint16_t* br = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] +
+                         (int64_t)(c - col_offset(L, j)) * sb_stride(rank, L.cap[j]);
+    // eight ranks per 16-byte load of each (rank offsets, capacities and row strides are multiples of 8); the chunk
+    // crossing the live rank keeps its live ranks only
+    float lora = 0.0f;
+    for (int q = 0; q < rank; q += 8) {
+      const uint4 mv = keep_first(*reinterpret_cast<const uint4*>(mr + q), rank - q);
+      const uint4 bv = keep_first(*reinterpret_cast<const uint4*>(br + q), rank - q);
+      lora = dot8(mv, bv, lora);
+    }
+    v += lora;
+  }
+  const uint16_t o = f32_to_bf16(v);
+  y[(int64_t)t * y_stride + c] = o;
+  if (last_out != nullptr && r.last_of[m] >= 0) last_out[(int64_t)r.last_of[m] * n_out + c] = o;
 }
 
 }  // namespace
