@@ -238,6 +238,8 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
                        f"{'finish_gated_kernel' if gated else 'finish_kernel'} (INT4 base + LoRA expand{fin})",
               "narrow": f"dec_kernel (INT4 base + fused LoRA expand{fin}; {ranges} input ranges"
                         + (", added by dec_reduce_kernel)" if ranges > 1 else ")"),
+              "rowtile": f"rowtile_kernel<{ranges}> (INT4 base + LoRA expand streamed with the input loop{fin}; "
+                         f"64 sorted rows x {64 * ranges} columns per workgroup)",
               "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[base]
     roof.update({"kernel": kernel, "group": f"layer0.{DOMINANT}", "launch_ms": kms, "reps": reps,
                  "route_ms_subtracted": route_ms, "flops_per_launch": kflops, "bytes_per_launch": kbytes})

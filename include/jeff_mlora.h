@@ -73,6 +73,10 @@ enum {
 #define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
 #define MLORA_FORCE_BASE_NARROW 32  /* narrow product (at most 256 tokens): every token in one row tile of 64 columns */
 #define MLORA_FORCE_RANGES(s) ((s) << 8)  /* a narrow product over s = 1, 2, 4 or 8 input ranges (s dividing k / 64) */
+/* row-tile product: 64 sorted rows x 64, 128 or 192 columns per workgroup, the LoRA second factor streamed with the
+ * input loop; group matrices whose widths are multiples of 16 (gated: gate and up widths multiples of 32) and rank
+ * capacities of at most 64 */
+#define MLORA_FORCE_BASE_ROWTILE 4096
 /* Epilogue flag: the group is a gate_up pair (matrix 0 gate, matrix 1 up, out / 2 columns each, out a multiple of
  * 256, one rank capacity of at most 64 for both); y (and last_out) receive silu(gate) * up, out / 2 columns per row,
  * each element

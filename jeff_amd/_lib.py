@@ -30,6 +30,7 @@ ROUTE_BAD_ADAPTER = 1
 ROUTE_BAD_SEQLENS = 2
 FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_SEGMENT, FORCE_SHRINK_MFMA, FORCE_BASE_SPLIT = 1, 2, 4, 8, 16
 FORCE_BASE_NARROW = 32
+FORCE_BASE_ROWTILE = 4096
 EPILOGUE_SILU_MUL = 64
 EPILOGUE_RESIDUAL = 128
 

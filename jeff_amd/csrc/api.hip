@@ -82,7 +82,7 @@ bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
   return long_segments(r, pool_rows);
 }
 
-enum class Base { gemv, fused, split, narrow };
+enum class Base { gemv, fused, split, narrow, rowtile };
 
 constexpr int64_t kNarrowMaxTokens = 256;  // the narrow kernel's row tile holds every token of the pass
 
@@ -102,6 +102,27 @@ int32_t gated_width(const mlora_int4_t* w, int32_t flags) {
 // The residual epilogue (MLORA_EPILOGUE_RESIDUAL): y holds the residual and receives residual + output.
 bool residual_of(int32_t flags) { return (flags & MLORA_EPILOGUE_RESIDUAL) != 0; }
 
+// CUs of the current device (256 when it cannot be asked, e.g. on a host without a GPU).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0 && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                        cus[dev] <= 0))
+    cus[dev] = 256;
+  return cus[dev];
+}
+
+// The row-tile product runs this group: column blocks for its widths and capacities, 32-bit x offsets.
+int rowtile_nb(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int32_t flags) {
+  return rowtile_blocks(*w, *L, r->tokens > 0 ? r->tokens : 1, gated_width(w, flags), device_cus());
+}
+bool rowtile_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride,
+                  int32_t flags) {
+  const int64_t row = x_stride > w->k ? x_stride : w->k;
+  return rowtile_nb(w, L, r, flags) > 0 && (r->tokens == 0 || row < ((int64_t)1 << 31) / r->tokens);
+}
+
 int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
             Base* out) {
   const bool gated = (flags & MLORA_EPILOGUE_SILU_MUL) != 0, resid = residual_of(flags);
@@ -117,13 +138,16 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
   } else if (flags & MLORA_FORCE_BASE_NARROW) {
     if (r->tokens > kNarrowMaxTokens || !split_fits(w, L, r, x_stride)) return MLORA_EUNSUPPORTED;
     *out = Base::narrow;
+  } else if (flags & MLORA_FORCE_BASE_ROWTILE) {
+    if (!rowtile_fits(w, L, r, x_stride, flags)) return MLORA_EUNSUPPORTED;
+    *out = Base::rowtile;
   } else if (flags & MLORA_FORCE_BASE_MFMA) {
     *out = Base::fused;
   } else if (r->tokens <= 8 && !gated && !resid) {  // (the GEMV kernel has no epilogues: few tokens take the tiles)
     *out = Base::gemv;
   } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
     *out = Base::fused;
-  } else {
+  } else {  // (the row-tile product runs when forced: on the decode shapes it is not yet faster than these)
     *out = r->tokens <= kNarrowMaxTokens ? Base::narrow : Base::split;
   }
   if (fs != 0 && *out != Base::narrow) return MLORA_EUNSUPPORTED;
@@ -148,16 +172,6 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
   return MLORA_OK;
 }
 
-// CUs of the current device (256 when it cannot be asked, e.g. on a host without a GPU).
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0 && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-                        cus[dev] <= 0))
-    cus[dev] = 256;
-  return cus[dev];
-}
 
 // Input ranges of a narrow product: the forced count, else the count S in {1, 2, 4, 8} (dividing the 64-input steps)
 // with the least estimated time. A workgroup takes about 0.85 us per step plus 8 us of fixed work (loads ahead of the
@@ -203,6 +217,9 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
              void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
   const int32_t inter = gated_width(w, flags);
   const bool resid = residual_of(flags);
+  if (base == Base::rowtile)
+    return launch_rowtile(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, rowtile_nb(w, L, r, flags), s,
+                          inter, resid);
   if (base == Base::narrow) {
     const int32_t ks = narrow_ranges(w, flags);
     const size_t need = dec_partials_bytes(*w, ks);
@@ -290,6 +307,9 @@ int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int
     L.n_mats = 2;
     L.cols[0] = L.cols[1] = out / 2;
     L.cap[0] = L.cap[1] = 8;
+  } else {  // one matrix of the group's width
+    L.n_mats = 1;
+    L.cols[0] = out;
   }
   mlora_route_t r = {};
   r.tokens = tokens;
@@ -297,9 +317,10 @@ int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int
   Base b;
   const int rc = base_of(&w, &L, &r, k, flags, &b);
   if (rc) return rc;
-  *base = b == Base::gemv ? 0 : b == Base::fused ? 1 : b == Base::split ? 2 : 3;
+  *base = b == Base::gemv ? 0 : b == Base::fused ? 1 : b == Base::split ? 2 : b == Base::narrow ? 3 : 4;
   *shrink = shrink_on_mfma(&r, pool_rows, flags) ? 1 : 0;
-  *ranges = b == Base::narrow ? narrow_ranges(&w, flags) : b == Base::split ? split_ranges(&w, tokens) : 1;
+  *ranges = b == Base::narrow ? narrow_ranges(&w, flags) : b == Base::split ? split_ranges(&w, tokens)
+            : b == Base::rowtile ? rowtile_nb(&w, &L, &r, flags) : 1;
   return MLORA_OK;
 }
 

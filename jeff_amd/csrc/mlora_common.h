@@ -175,8 +175,7 @@ __device__ __forceinline__ int live_rank(const mlora_lora_t& L, int a, int j) {
 // of two, at least 8, at most cap_j (a rank-0 row keeps stride min(8, cap_j), so reads that ignore the rank stay in
 // the block). Low-rank adapters' rows are then dense: a rank-8 row is 16 bytes, not cap_j * 2.
 __device__ __forceinline__ int sb_stride(int rank, int cap) {
-  int s = 8;
-  while (s < rank) s <<= 1;
+  const int s = rank <= 8 ? 8 : 1 << (32 - __builtin_clz((unsigned)(rank - 1)));
   return s < cap ? s : cap;
 }
 
@@ -245,6 +244,13 @@ int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
                bool residual = false);
+// Row-tile product (64 sorted rows x 64 nb columns per workgroup, the LoRA second factor streamed with the K loop):
+// the column blocks per wave for this group (0: the kernel cannot run it), and the launch (residual as above, not
+// gated).
+int rowtile_blocks(const mlora_int4_t& w, const mlora_lora_t& L, int64_t tokens, int32_t inter, int cus);
+int launch_rowtile(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
+                   int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
+                   const uint16_t* mid, int nb, hipStream_t stream, int32_t inter = 0, bool residual = false);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

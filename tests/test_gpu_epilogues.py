@@ -125,10 +125,14 @@ def test_epilogues_refuse_bad_arguments() -> None:
 
 
 FUSED_CASES = {  # name: (tokens per request, requests, adapters, gate/up width, inputs, tiles, the kernel chosen)
+    "decode-rowtile": (1, 160, 12, 512, 2048, "rowtile", "rowtile"),
+    "decode-rowtile-wide": (1, 256, 64, 6144, 2048, "rowtile", "rowtile"),  # 192-column tiles, one per CU
     "decode-narrow": (1, 160, 12, 512, 2048, None, "narrow"),
     "decode-narrow-ranges": (1, 96, 12, 256, 1024, "narrow-4", "narrow"),
     "decode-few-tokens": (1, 5, 12, 256, 512, "narrow", "narrow"),
+    "decode-few-tokens-rowtile": (1, 5, 12, 256, 512, "rowtile", "rowtile"),
     "decode-split": (1, 600, 48, 256, 1024, None, "split"),
+    "decode-rowtile-many": (1, 600, 48, 256, 1024, "rowtile", "rowtile"),
     "prefill-fused": (64, 24, 12, 384, 1024, None, "mfma"),
     "prefill-tail": (40, 26, 12, 128, 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
 }
@@ -137,8 +141,8 @@ FUSED_CASES = {  # name: (tokens per request, requests, adapters, gate/up width,
 @pytest.mark.parametrize("name", list(FUSED_CASES))
 def test_silu_mul_in_the_product_tile_equals_silu_mul_of_the_product(name: str) -> None:
     """int4_product(..., epilogue="silu_mul") on a gate_up group (gate then up, one width) against silu_mul of the
-    plain product (the same tiles), bit for bit, for every kernel family that takes it (narrow with and without input
-    ranges, few tokens, split, the 256 x 256 tiles with a partial last tile), with the last-token rows gathered; and
+    plain product (the same tiles), bit for bit, for every kernel family that takes it (row tiles of 64 and 192
+    columns, narrow with and without input ranges, few tokens, split, the 256 x 256 tiles with a partial last tile), with the last-token rows gathered; and
     against the oracle's silu_mul of the plain product."""
     from jeff_amd.fast_path import Workspace
     from jeff_amd.int4_kernels import int4_product
@@ -159,10 +163,13 @@ def test_silu_mul_in_the_product_tile_equals_silu_mul_of_the_product(name: str) 
     x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
     ws = Workspace(tokens, row_len, max_rank=lin.rank)
     tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-4": Int4Tiles("narrow", "segment", 4),
+             "split": Int4Tiles("split", "segment"), "rowtile": Int4Tiles("rowtile", "segment"),
              "mfma": Int4Tiles("mfma", "mfma")}[forced]
     flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_SILU_MUL
     assert int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)[0] == kernel
-    plain = int4_product(lin, x, ws, adp, tiles=tiles)
+    # the plain product on the same kernels (unforced, a few tokens would take the GEMV, which sums in another order)
+    plan = int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)
+    plain = int4_product(lin, x, ws, adp, tiles=tiles if tiles is not None else Int4Tiles(plan[0], plan[1]))
     last = torch.zeros(requests, width, dtype=torch.bfloat16, device="cuda")
     fused = int4_product(lin, x, ws, adp, tiles=tiles, last_out=last, epilogue="silu_mul")
     assert fused.shape == (tokens, width)
@@ -187,10 +194,13 @@ def test_silu_mul_epilogue_refusals() -> None:
 
 
 RESIDUAL_CASES = {  # name: (tokens per request, requests, adapters, matrix widths, inputs, tiles, the kernel chosen)
+    "decode-rowtile": (1, 160, 12, [512], 2048, "rowtile", "rowtile"),
+    "decode-rowtile-two": (1, 256, 64, [1024, 1024], 6144, "rowtile", "rowtile"),  # the down product's inputs
     "decode-narrow": (1, 160, 12, [512], 2048, None, "narrow"),
     "decode-narrow-ranges": (1, 96, 12, [256], 1024, "narrow-4", "narrow"),
     "decode-few-tokens": (1, 5, 12, [256], 512, None, "narrow"),  # 5 tokens: the narrow product, not the GEMV
     "decode-split": (1, 600, 48, [256], 1024, None, "split"),
+    "decode-rowtile-many": (1, 600, 48, [256], 1024, "rowtile", "rowtile"),
     "prefill-fused": (64, 24, 12, [384, 128], 1024, None, "mfma"),
     "prefill-small": (20, 6, 12, [256], 512, "mfma", "mfma"),  # 120 tokens: still the 256 x 256 kernel
     "prefill-tail": (40, 26, 12, [128], 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
@@ -218,7 +228,9 @@ def test_residual_add_in_the_product_tile_equals_add_rms_of_the_product(name: st
     adp = torch.tensor(rng.integers(0, adapters + 1, requests).astype(np.int32), device="cuda")
     x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
     ws = Workspace(tokens, row_len, max_rank=lin.rank)
-    tiles = {None: None, "narrow-4": Int4Tiles("narrow", "segment", 4), "mfma": Int4Tiles("mfma", "mfma")}[forced]
+    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-4": Int4Tiles("narrow", "segment", 4),
+             "split": Int4Tiles("split", "segment"), "rowtile": Int4Tiles("rowtile", "segment"),
+             "mfma": Int4Tiles("mfma", "mfma")}[forced]
     flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_RESIDUAL
     plan = int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)
     assert plan[0] == kernel

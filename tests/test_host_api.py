@@ -130,6 +130,12 @@ def test_kernel_choice_rule() -> None:
     assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("narrow", "segment")
     assert int4_tiles(4096, 2048, 257, 257, 65) == Int4Tiles("split", "segment")
     assert int4_tiles(12288, 2048, 4096, 4096, 1025) == Int4Tiles("split", "segment")
+    from jeff_amd import _lib
+    from jeff_amd.int4_tiles import int4_plan
+    # the row-tile product when forced: column blocks per wave chosen to give every CU a workgroup (12288 columns
+    # cut into 192-column tiles, 4096 into 64-column ones)
+    assert int4_plan(4096, 2048, 256, 256, 65, flags=_lib.FORCE_BASE_ROWTILE) == ("rowtile", "segment", 1)
+    assert int4_plan(12288, 2048, 256, 256, 65, flags=_lib.FORCE_BASE_ROWTILE) == ("rowtile", "segment", 3)
     assert int4_tiles(3072, 1024, 8704, 64, 17) == Int4Tiles("mfma", "mfma")
     with pytest.raises(ValueError):
         int4_tiles(100, 1024, 4)
