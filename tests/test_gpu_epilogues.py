@@ -90,6 +90,31 @@ def test_silu_mul(rows: int, inter: int) -> None:
     torch.testing.assert_close(y.float(), want.float(), rtol=BF16_STEP, atol=1e-6)
 
 
+def test_silu_mul_over_every_bf16_gate() -> None:
+    """All 65536 bf16 gate values (with up = 1, then random ups): bit for bit the oracle's rounding wherever exp(-g)
+    is finite in float32; below g of about -88.7, where the reference's float32 formula overflows exp and gives
+    g / inf = -0, bit for bit that formula (the float64 oracle keeps a tiny nonzero value there)."""
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
+    gf = from_bits(g).float()
+    with np.errstate(over="ignore", invalid="ignore"):
+        overflow = np.isinf(np.exp(-gf.numpy()))
+    overflow &= gf.numpy() < 0  # exp(-g) overflows: g below about -88.7 (and g = -inf)
+    ups = [np.full((256, 256), 0x3F80, np.uint16),
+           bits(torch.randn(256, 256, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16))]
+    for u in ups:
+        gu = np.concatenate([g, u], 1)
+        y = bits(silu_mul(from_bits(gu).cuda()))
+        with np.errstate(invalid="ignore"):  # the NaN and infinite gates
+            _, want, _ = oracle_silu_mul(gu)
+        uf = from_bits(u).float()
+        f32 = bits(((gf / (1.0 + torch.exp(-gf))).to(torch.bfloat16).float() * uf).to(torch.bfloat16))
+        want = np.where(overflow, f32, want)
+        nan_got, nan_want = np.isnan(from_bits(y).float().numpy()), np.isnan(from_bits(want).float().numpy())
+        assert np.array_equal(nan_got, nan_want)
+        differ = (y != want) & ~nan_got
+        assert not differ.any(), f"{int(differ.sum())} gates differ, e.g. {[hex(v) for v in g[differ][:8]]}"
+
+
 def test_epilogues_are_deterministic_and_replay_in_a_graph() -> None:
     x, d, w1 = case(256, 2048, 9)
     gu = torch.randn(256, 12288, device="cuda").to(torch.bfloat16)
