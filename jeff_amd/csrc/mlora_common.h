@@ -73,22 +73,17 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_ca
 // g rcp(d) corrected once by its exact residual (fma(-q0, d, g), exact while q0 is within a few ulps of g / d):
 // q0 + residual rcp(d), rounded once, is the correctly rounded quotient except within about 2^-22 ulp of a rounding
 // boundary (a bare reciprocal, within 1 ulp, misrounds values within an ulp of a bf16 rounding midpoint). Where d
-// reaches 2^64 (g below about -44) the quotient is formed for d 2^-64 and scaled back by 2^-64, both exact (powers
-// of two, every value normal), so the reciprocal never falls among the denormals, which it flushes; d = inf (g below
-// about -88.7) gives g / inf = -0, as the float32 formula does; the quotient takes the sign of g (so -0 gives -0) and
-// g = +inf gives +inf. No branch: the products apply this to 64 values per thread, and a branch per value serialises
-// their chains.
+// reaches 2^120 (g below about -83: the reciprocal would fall among the denormals, which it flushes) the quotient is
+// an IEEE division.
 __device__ __forceinline__ float bf16_round(float v) {
   return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v) << 16);
 }
 __device__ __forceinline__ float silu_quotient(float g) {
   const float d = 1.0f + __expf(-g);
-  const float sc = d >= 0x1p64f ? 0x1p-64f : 1.0f;
-  const float ds = d * sc;
-  const float r = __builtin_amdgcn_rcpf(ds);
+  if (__builtin_expect(!(d < 0x1p120f), 0)) return g / d;
+  const float r = __builtin_amdgcn_rcpf(d);
   const float q0 = g * r;
-  const float q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, ds, g), r, q0) * sc, g);
-  return d == __builtin_inff() ? 0.0f * g : g == __builtin_inff() ? g : q;
+  return __builtin_fmaf(__builtin_fmaf(-q0, d, g), r, q0);
 }
 __device__ __forceinline__ uint4 silu_mul8(uint4 g, uint4 u) {
   const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
