@@ -318,46 +318,62 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
           }
         };
-        // Chunks wholly inside the live rank go in unmasked; the one chunk crossing it (rk not a multiple of 16)
-        // keeps its live ranks in both operands. Rows outside the segment get zero first factors.
-        auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
-          if (rk <= 0) return;
-          bool mine[kDMB];
+        // Each row's first factors past its own segment's live rank are set to zero once, here (the segment's live rank
+        // from its lane of llive, or from memory past the wave's first 64 segments; rows past the pass have none): a
+        // segment's term then needs only a row mask on the first factors, and the sB chunk crossing the live rank (rk
+        // not a multiple of 16) keeps only its live ranks, so the sB row's padding never enters the sum.
 #pragma unroll
-          for (int mb = 0; mb < kDMB; ++mb) mine[mb] = rseg[mb] == s;
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            if (16 * k16 >= rk) break;
-            const bool edge = 16 * k16 + 16 > rk;
-            const int n = rk - (16 * k16 + 8 * (lane >> 5));
-            uint4 bm = edge ? keep_first(bv[k16], n) : bv[k16];
-            if (!allin) bm = cin ? bm : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int mb = 0; mb < kDMB; ++mb) {
-              if (s < blo[mb] || s > bhi[mb]) continue;
-              uint4 am = mine[mb] ? m[mb][k16] : make_uint4(0, 0, 0, 0);
-              if (edge) am = keep_first(am, n);
-              acc[mb] = mfma32(bm, am, acc[mb]);
-            }
+        for (int mb = 0; mb < kDMB; ++mb) {
+          const int sq = rseg[mb] - s_lo;
+          int rrow = __builtin_amdgcn_ds_bpermute((sq & 63) << 2, llive);
+          if (rseg[mb] >= 0 && sq >= kWave) {
+            const int a = r.seg_adapter[rseg[mb]];
+            rrow = a == 0 ? 0 : live_rank(L, a, j);
           }
-        };
-        uint4 q0[4], q1[4], q2[4], q3[4];
-        int k0, k1, k2, k3;
-        // input range ks takes segments s_lo + ks, s_lo + ks + S, ... (the ranges' sums are added afterwards)
-        const int S = ksplit;
-        load_b(s_lo + ks, q0, k0);
-        load_b(s_lo + ks + S, q1, k1);
-        load_b(s_lo + ks + 2 * S, q2, k2);
-        load_b(s_lo + ks + 3 * S, q3, k3);
-        for (int s = s_lo + ks; s <= s_hi; s += 4 * S) {
-          apply(s, q0, k0);
-          load_b(s + 4 * S, q0, k0);
-          apply(s + S, q1, k1);
-          load_b(s + 5 * S, q1, k1);
-          apply(s + 2 * S, q2, k2);
-          load_b(s + 6 * S, q2, k2);
-          apply(s + 3 * S, q3, k3);
-          load_b(s + 7 * S, q3, k3);
+          if (rseg[mb] < 0) rrow = 0;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16)
+            m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
+        }
+        {
+          auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+            if (rk <= 0) return;
+            uint32_t rmask[kDMB];
+#pragma unroll
+            for (int mb = 0; mb < kDMB; ++mb) rmask[mb] = rseg[mb] == s ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) {
+              if (16 * k16 >= rk) break;
+              uint4 bm = bv[k16];
+              if (16 * k16 + 16 > rk) bm = keep_first(bm, rk - (16 * k16 + 8 * (lane >> 5)));
+              if (!allin) bm = cin ? bm : make_uint4(0, 0, 0, 0);
+#pragma unroll
+              for (int mb = 0; mb < kDMB; ++mb) {
+                if (s < blo[mb] || s > bhi[mb]) continue;
+                const uint4 am = make_uint4(m[mb][k16].x & rmask[mb], m[mb][k16].y & rmask[mb],
+                                            m[mb][k16].z & rmask[mb], m[mb][k16].w & rmask[mb]);
+                acc[mb] = mfma32(bm, am, acc[mb]);
+              }
+            }
+          };
+          uint4 q0[4], q1[4], q2[4], q3[4];
+          int k0, k1, k2, k3;
+          // input range ks takes segments s_lo + ks, s_lo + ks + S, ... (the ranges' sums are added afterwards)
+          const int S = ksplit;
+          load_b(s_lo + ks, q0, k0);
+          load_b(s_lo + ks + S, q1, k1);
+          load_b(s_lo + ks + 2 * S, q2, k2);
+          load_b(s_lo + ks + 3 * S, q3, k3);
+          for (int s = s_lo + ks; s <= s_hi; s += 4 * S) {
+            apply(s, q0, k0);
+            load_b(s + 4 * S, q0, k0);
+            apply(s + S, q1, k1);
+            load_b(s + 5 * S, q1, k1);
+            apply(s + 2 * S, q2, k2);
+            load_b(s + 6 * S, q2, k2);
+            apply(s + 3 * S, q3, k3);
+            load_b(s + 7 * S, q3, k3);
+          }
         }
       }
     }
