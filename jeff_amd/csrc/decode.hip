@@ -318,23 +318,6 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
           }
         };
-        // Each row's first factors past its own segment's live rank are set to zero once, here (the segment's live rank
-        // from its lane of llive, or from memory past the wave's first 64 segments; rows past the pass have none): a
-        // segment's term then needs only a row mask on the first factors, and the sB chunk crossing the live rank (rk
-        // not a multiple of 16) keeps only its live ranks, so the sB row's padding never enters the sum.
-#pragma unroll
-        for (int mb = 0; mb < kDMB; ++mb) {
-          const int sq = rseg[mb] - s_lo;
-          int rrow = __builtin_amdgcn_ds_bpermute((sq & 63) << 2, llive);
-          if (rseg[mb] >= 0 && sq >= kWave) {
-            const int a = r.seg_adapter[rseg[mb]];
-            rrow = a == 0 ? 0 : live_rank(L, a, j);
-          }
-          if (rseg[mb] < 0) rrow = 0;
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16)
-            m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
-        }
         {
           auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
             if (rk <= 0) return;
@@ -364,6 +347,24 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
           load_b(s_lo + ks + S, q1, k1);
           load_b(s_lo + ks + 2 * S, q2, k2);
           load_b(s_lo + ks + 3 * S, q3, k3);
+          // Each row's first factors past its own segment's live rank are set to zero once, while the first segments'
+          // sB loads are in flight (the segment's live rank from its lane of llive, or from memory past the wave's
+          // first 64 segments; rows past the pass have none): a segment's term then needs only a row mask on the first
+          // factors, and the sB chunk crossing the live rank (rk not a multiple of 16) keeps only its live ranks, so
+          // the sB row's padding never enters the sum.
+#pragma unroll
+          for (int mb = 0; mb < kDMB; ++mb) {
+            const int sq = rseg[mb] - s_lo;
+            int rrow = __builtin_amdgcn_ds_bpermute((sq & 63) << 2, llive);
+            if (rseg[mb] >= 0 && sq >= kWave) {
+              const int a = r.seg_adapter[rseg[mb]];
+              rrow = a == 0 ? 0 : live_rank(L, a, j);
+            }
+            if (rseg[mb] < 0) rrow = 0;
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16)
+              m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
+          }
           for (int s = s_lo + ks; s <= s_hi; s += 4 * S) {
             apply(s, q0, k0);
             load_b(s + 4 * S, q0, k0);
