@@ -4,10 +4,10 @@
 // rows x 64 columns, so a product spreads over the CUs with few or no splits of the input dimension (a 12288-column
 // product runs as 192 workgroups over all 2048 inputs). 8 waves in 4 row groups x 2 column groups: a wave owns 64
 // rows x 32 columns (two 32x32 MFMA blocks). A step's packed words are loaded and dequantised once for the
-// workgroup (one word per thread) into an LDS buffer that every wave reads its weight operands from, and each wave
-// reads its 64 rows of x from an LDS ring that buffer loads with the LDS flag fill, as in the prefill kernel; words
-// and x rows are loaded three steps ahead, and the step's barrier sits in its middle, so the operand reads of each
-// half of a step overlap the other half's MFMAs.
+// workgroup (one word per thread) into a ring of LDS buffers that every wave reads its weight operands from, and
+// each wave reads its 64 rows of x from an LDS ring that buffer loads with the LDS flag fill, as in the prefill kernel;
+// words and x rows are loaded three steps ahead, the step's barrier sits in its middle, so the operand reads of each
+// half of a step overlap the other half's MFMAs, and a step's words are dequantised two steps ahead, past a barrier.
 // When the columns alone are too few for the CUs, the input dimension is split into S ranges: each range writes its
 // float32 tile in the accumulators' own order (one coalesced 1 KB store per MFMA block and column group), and
 // dec_reduce_kernel adds the ranges in order and rounds once.
@@ -43,6 +43,7 @@ __shared__ __attribute__((aligned(16))) uint16_t d_x2[kDRows * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t d_x3[kDRows * kTK];
 __shared__ uint4 d_w0[8 * kDCols];  // a step's weights, dequantised: 8 input octets x 64 columns of 8 bf16
 __shared__ uint4 d_w1[8 * kDCols];
+__shared__ uint4 d_w2[8 * kDCols];
 __shared__ int32_t d_orig[kDRows];  // the tile's rows: original token index, -1 past the tokens
 __shared__ int32_t d_last[kDRows];  // the tile's rows: request whose last token it is, else -1
 
@@ -195,14 +196,14 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     load_mid(m0, jlo, 0);
   }
 
-  // Step i reads x buffer i % 4 (its rows loaded at the start of step i - 3) and dequantised weight buffer i % 2
-  // (written during step i - 1 from the words loaded at the start of step i - 3): a step of this narrow tile is short
-  // (8 MFMAs per wave), so the loads run three steps ahead. Every load is unconditional (past the last step it
-  // re-reads the last one), so the number of loads in flight at each wait is the same on every path; a step's words
-  // are issued before its x rows (loads complete in order).
+  // Step i reads x buffer i % 4 (its rows loaded at the start of step i - 3) and dequantised weight buffer i % 3
+  // (written late in step i - 2, after that step's barrier, from the words loaded at the start of step i - 3 into
+  // register stage i % 3): a step of this narrow tile is short (8 MFMAs per wave), so the loads run three steps
+  // ahead. Every load is unconditional (past the last step it re-reads the last one), so the number of loads in flight
+  // at each wait is the same on every path; a step's words are issued before its x rows (loads complete in order).
   const int nk = w.k / kTK / ksplit;  // this block's K steps, from step ks * nk
   const int kbase = ks * nk * kTK;
-  WStage s0, s1, s2, s3;
+  WStage s0, s1, s2;
   fetch_w(s0, kbase);
   dma_x(d_x0, kbase);
   fetch_w(s1, kbase + min(1, nk - 1) * kTK);
@@ -225,22 +226,27 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   // landed: step 0's words and x rows and step 1's words (step 1's x rows and step 2's loads may be in flight)
   MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
   dequant_to(d_w0, s0);
+  dequant_to(d_w1, s1);
   step_sync();
   uint4 a01[2][kDMB], b01[2];  // the first half of the current step's operands, read after the previous barrier
   read_half(d_x0, d_w0, 0, a01, b01);
   // One barrier per step, in its middle: the second half of step i's operands is read while the first half's MFMAs
   // run, and the first half of step i + 1's after the barrier, while the second half's MFMAs run. Before the barrier
-  // the wave issues step i + 3's loads (words before x rows: loads complete in order) and dequantises step i + 1's
-  // words into the weight buffer step i - 1 read; the barrier then makes step i + 1's x rows and weights visible.
+  // the wave issues step i + 3's loads (words before x rows: loads complete in order) and waits only for step i + 1's
+  // x rows; the barrier makes them visible, with step i + 1's weights (written in step i - 1). Past the barrier,
+  // beside the second half's MFMAs, the wave dequantises step i + 2's words into the weight buffer step i - 1 read, so
+  // the conversion is off the path from one barrier to the next.
   auto run = [&](auto slot, int i) __attribute__((always_inline)) {
-    constexpr int B = decltype(slot)::value;
-    const uint16_t* xs = B == 0 ? d_x0 : B == 1 ? d_x1 : B == 2 ? d_x2 : d_x3;
-    const uint16_t* xn = B == 0 ? d_x1 : B == 1 ? d_x2 : B == 2 ? d_x3 : d_x0;  // buffer (i + 1) % 4
-    uint16_t* xf = B == 0 ? d_x3 : B == 1 ? d_x0 : B == 2 ? d_x1 : d_x2;        // buffer (i + 3) % 4
-    WStage& wn = B == 0 ? s1 : B == 1 ? s2 : B == 2 ? s3 : s0;                  // step i + 1's words
-    WStage& wf = B == 0 ? s3 : B == 1 ? s0 : B == 2 ? s1 : s2;                  // step i + 3's words (fetched now)
-    const uint4* wcur = (B & 1) ? d_w1 : d_w0;
-    uint4* wnext = (B & 1) ? d_w0 : d_w1;
+    constexpr int B = decltype(slot)::value;  // i % 12
+    constexpr int X = B % 4, W = B % 3;
+    const uint16_t* xs = X == 0 ? d_x0 : X == 1 ? d_x1 : X == 2 ? d_x2 : d_x3;
+    const uint16_t* xn = X == 0 ? d_x1 : X == 1 ? d_x2 : X == 2 ? d_x3 : d_x0;  // buffer (i + 1) % 4
+    uint16_t* xf = X == 0 ? d_x3 : X == 1 ? d_x0 : X == 2 ? d_x1 : d_x2;        // buffer (i + 3) % 4
+    WStage& wf = W == 0 ? s0 : W == 1 ? s1 : s2;       // step i + 3's words (fetched now into stage i % 3)
+    WStage& wdq = W == 0 ? s2 : W == 1 ? s0 : s1;      // step i + 2's words (dequantised now)
+    const uint4* wcur = W == 0 ? d_w0 : W == 1 ? d_w1 : d_w2;
+    const uint4* wnext = W == 0 ? d_w1 : W == 1 ? d_w2 : d_w0;  // buffer (i + 1) % 3
+    uint4* wfar = W == 0 ? d_w2 : W == 1 ? d_w0 : d_w1;         // buffer (i + 2) % 3
     uint4 a23[2][kDMB], b23[2];
     read_half(xs, wcur, 2, a23, b23);
     mfma_k16(a01[0], b01[0]);
@@ -249,21 +255,23 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     mfma_k16(a01[1], b01[1]);
     dma_x(xf, kbase + min(i + 3, nk - 1) * kTK);
     __builtin_amdgcn_sched_barrier(0);
-    // landed: step i + 1's words and x rows (step i + 2's and i + 3's loads in flight)
+    // landed: step i + 1's x rows (step i + 2's and i + 3's loads in flight)
     MLORA_WAIT_VM(kDWLoads + kDXLoads + kDWLoads + kDXLoads);
     __builtin_amdgcn_sched_barrier(0);
-    dequant_to(wnext, wn);
     step_sync();
     read_half(xn, wnext, 0, a01, b01);  // past the last step: re-reads of valid buffers, unused
     __builtin_amdgcn_sched_barrier(0);
     mfma_k16(a23[0], b23[0]);
     mfma_k16(a23[1], b23[1]);
+    // landed: step i + 2's words (its x rows and step i + 3's loads in flight)
+    MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
+    dequant_to(wfar, wdq);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  for (int it = 0; it < nk; it += 4) {
+  for (int it = 0; it < nk; it += 12) {
     run(I0{}, it);
     if (it == 0 && lora) llive0 = la == 0 ? 0 : live_rank(L, la, jlo);  // lands during the next steps
     if (it + 1 >= nk) break;
@@ -272,6 +280,22 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     run(I2{}, it + 2);
     if (it + 3 >= nk) break;
     run(I3{}, it + 3);
+    if (it + 4 >= nk) break;
+    run(std::integral_constant<int, 4>{}, it + 4);
+    if (it + 5 >= nk) break;
+    run(std::integral_constant<int, 5>{}, it + 5);
+    if (it + 6 >= nk) break;
+    run(std::integral_constant<int, 6>{}, it + 6);
+    if (it + 7 >= nk) break;
+    run(std::integral_constant<int, 7>{}, it + 7);
+    if (it + 8 >= nk) break;
+    run(std::integral_constant<int, 8>{}, it + 8);
+    if (it + 9 >= nk) break;
+    run(std::integral_constant<int, 9>{}, it + 9);
+    if (it + 10 >= nk) break;
+    run(std::integral_constant<int, 10>{}, it + 10);
+    if (it + 11 >= nk) break;
+    run(std::integral_constant<int, 11>{}, it + 11);
   }
   MLORA_WAIT_VM(0);
 
