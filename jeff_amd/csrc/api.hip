@@ -174,10 +174,10 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
 
 
 // Input ranges of a narrow product: the forced count, else the count S in {1, 2, 4, 8} (dividing the 64-input steps)
-// with the least estimated time. A workgroup takes about 0.85 us per step plus 8 us of fixed work (loads ahead of the
-// first step, the LoRA term, the stores), in rounds of one per CU; a split adds a launch (4 us) and the float32
-// ranges' round trip through memory at 5 TB/s. (Measured on decode-28l's groups, the estimate picks the fastest
-// count or one within 1%.)
+// with the least estimated time. A workgroup takes about 0.6 us per step plus 12 us of fixed work (loads ahead of the
+// first step, the LoRA term, the stores), in rounds of one per CU; a split adds 2 us (the reduction's launch) and the
+// float32 ranges' round trip through memory at 5 TB/s. (Fitted to 256-token products of 2048 -> 4096, 2048 -> 2048
+// and 6144 -> 2048 columns over 1, 2, 4 and 8 ranges; the estimate picks the fastest count of each: 4, 4 and 8.)
 int32_t narrow_ranges(const mlora_int4_t* w, int32_t flags) {
   if ((flags >> 8) & 0xF) return (flags >> 8) & 0xF;  // forced (base_of checked it)
   const int64_t tiles = w->columns / 64, steps = w->k / 64, cus = device_cus();
@@ -186,8 +186,8 @@ int32_t narrow_ranges(const mlora_int4_t* w, int32_t flags) {
   for (int32_t s = 1; s <= 8; s *= 2) {
     if (steps % s) continue;
     const int64_t rounds = (tiles * s + cus - 1) / cus;
-    double t = (double)rounds * (0.85 * (double)(steps / s) + 8.0);
-    if (s > 1) t += 4.0 + (double)dec_partials_bytes(*w, s) * 2.0 / 5.0e6;
+    double t = (double)rounds * (0.6 * (double)(steps / s) + 12.0);
+    if (s > 1) t += 2.0 + (double)dec_partials_bytes(*w, s) * 2.0 / 5.0e6;
     if (s == 1 || t < best) {
       best = t;
       pick = s;
