@@ -34,6 +34,7 @@ constexpr int kDXLoads = 4;               // x rows: LDS-flag buffer loads per l
 constexpr int kDWLoads = 3;               // weights: a word, a scale and a zero point per thread and step
 constexpr int kDRankChunk = 64;           // ranks of a matrix per LoRA pass
 constexpr int kDRedThreads = 256;
+constexpr int kDMaxRanges = 8;            // input ranges of a narrow product (the host allows 1, 2, 4 or 8)
 
 static_assert(kDRows / kDRG == 32 * kDMB, "row groups must cover the tile");
 
@@ -493,16 +494,23 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_kernel(const float4* 
   const int row = (wave / kDCG) * 32 * kDMB + mb * 32 + (lane & 31);
   const int col = nt * kDCols + (wave % kDCG) * 32 + g * 8 + (lane >> 5) * 4;
   if (row >= r.tokens || col >= n_out) return;
-  float4 v = part[f];
-  for (int ks = 1; ks < ksplit; ++ks) {
-    const float4 u = part[(int64_t)ks * per + f];
-    v.x += u.x;
-    v.y += u.y;
-    v.z += u.z;
-    v.w += u.w;
-  }
+  // every range's float4, then the row's token order, are loaded before the first add (one memory latency, not one
+  // per range), then the ranges are added in order
+  float4 u[kDMaxRanges];
+#pragma unroll
+  for (int ks = 0; ks < kDMaxRanges; ++ks)
+    if (ks < ksplit) u[ks] = part[(int64_t)ks * per + f];
   const int64_t orig = r.tok_perm[row];
   const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
+  float4 v = u[0];
+#pragma unroll
+  for (int ks = 1; ks < kDMaxRanges; ++ks)
+    if (ks < ksplit) {
+      v.x += u[ks].x;
+      v.y += u[ks].y;
+      v.z += u[ks].z;
+      v.w += u[ks].w;
+    }
   store4(y + orig * y_stride + col, lq >= 0 ? last_out + lq * n_out + col : nullptr, pack_bf16x2(v.x, v.y),
          pack_bf16x2(v.z, v.w), n_out - col, vec);
 }
@@ -529,23 +537,32 @@ __global__ __launch_bounds__(kDRedThreads) void dec_reduce_gated_kernel(const fl
   if (row >= r.tokens) return;
   const int64_t fg = part_index(0, n_tiles, nt, rg * kDCG, mb, g, lane);
   const int64_t fu = part_index(0, n_tiles, nt, rg * kDCG + 1, mb, g, lane);
-  float4 gv = part[fg], uv = part[fu];
-  for (int ks = 1; ks < ksplit; ++ks) {
-    const float4 a = part[(int64_t)ks * per + fg], b = part[(int64_t)ks * per + fu];
-    gv.x += a.x;
-    gv.y += a.y;
-    gv.z += a.z;
-    gv.w += a.w;
-    uv.x += b.x;
-    uv.y += b.y;
-    uv.z += b.z;
-    uv.w += b.w;
-  }
+  // all loads first (every range's gate and up float4s, then the row's token order), then the ranges added in order
+  float4 a[kDMaxRanges], b[kDMaxRanges];
+#pragma unroll
+  for (int ks = 0; ks < kDMaxRanges; ++ks)
+    if (ks < ksplit) {
+      a[ks] = part[(int64_t)ks * per + fg];
+      b[ks] = part[(int64_t)ks * per + fu];
+    }
+  const int64_t orig = r.tok_perm[row];
+  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
+  float4 gv = a[0], uv = b[0];
+#pragma unroll
+  for (int ks = 1; ks < kDMaxRanges; ++ks)
+    if (ks < ksplit) {
+      gv.x += a[ks].x;
+      gv.y += a[ks].y;
+      gv.z += a[ks].z;
+      gv.w += a[ks].w;
+      uv.x += b[ks].x;
+      uv.y += b[ks].y;
+      uv.z += b[ks].z;
+      uv.w += b[ks].w;
+    }
   const uint2 v = silu_mul4(make_uint2(pack_bf16x2(gv.x, gv.y), pack_bf16x2(gv.z, gv.w)),
                             make_uint2(pack_bf16x2(uv.x, uv.y), pack_bf16x2(uv.z, uv.w)));
   const uint32_t lo = v.x, hi = v.y;
-  const int64_t orig = r.tok_perm[row];
-  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
   if (vec & kStoreVec) {
     *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
     if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
@@ -569,6 +586,7 @@ int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter, bool residual) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
+  if (ksplit < 1 || ksplit > kDMaxRanges) return MLORA_EINVAL;
   if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit || (residual && inter > 0)) return MLORA_EINVAL;
   if (inter > 0 && (inter % 32 || n_out != 2 * inter)) return MLORA_EINVAL;
   if (ksplit > 1 && part == nullptr) return MLORA_EWORKSPACE;
