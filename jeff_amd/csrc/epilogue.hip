@@ -13,6 +13,8 @@ using namespace mlora;
 
 constexpr int kRmsRows = 4;                          // rows (waves) per workgroup
 constexpr int kRmsChunks = MLORA_EPILOGUE_MAX_N / 512;  // 16-byte chunks per lane at the largest row
+constexpr int kRmsGroup = 2;                            // chunks per lane whose loads are issued together
+static_assert(kRmsChunks % kRmsGroup == 0, "whole groups of chunks");
 
 __device__ __forceinline__ float wave_sum_fixed(float v) {
 #pragma unroll
@@ -33,43 +35,67 @@ __global__ __launch_bounds__(kRmsRows * 64) void add_rms_kernel(const uint16_t* 
   const uint16_t* xr = x + row * x_stride;
   float v[kRmsChunks][8];
   float ss = 0.0f;
+  // The lane's chunks are taken kRmsGroup at a time: the group's x and d loads are all issued before the first is
+  // used (one memory latency per group, not two per chunk); the sums run in chunk order as before.
 #pragma unroll
-  for (int i = 0; i < kRmsChunks; ++i) {
-    const int c = lane + 64 * i;
-    if (c >= chunks) break;
-    const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  for (int i0 = 0; i0 < kRmsChunks; i0 += kRmsGroup) {
+    if (lane + 64 * i0 >= chunks) break;
+    uint4 xv[kRmsGroup], dv[kRmsGroup];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[i][e] = (e & 1) ? bf16_hi(xw[e >> 1]) : bf16_lo(xw[e >> 1]);
-    if (d != nullptr) {
-      const uint4 dv = *reinterpret_cast<const uint4*>(d + row * d_stride + 8 * c);
-      const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
-      uint32_t ow[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const uint32_t p = pack_bf16x2(v[i][e] + bf16_lo(dw[e >> 1]), v[i][e + 1] + bf16_hi(dw[e >> 1]));
-        ow[e >> 1] = p;
-        v[i][e] = bf16_lo(p);
-        v[i][e + 1] = bf16_hi(p);
+    for (int u = 0; u < kRmsGroup; ++u) {
+      const int c = lane + 64 * (i0 + u);
+      if (c < chunks) {
+        xv[u] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+        if (d != nullptr) dv[u] = *reinterpret_cast<const uint4*>(d + row * d_stride + 8 * c);
       }
-      *reinterpret_cast<uint4*>(xo + row * xo_stride + 8 * c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+    for (int u = 0; u < kRmsGroup; ++u) {
+      const int i = i0 + u, c = lane + 64 * i;
+      if (c >= chunks) break;
+      const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[i][e] = (e & 1) ? bf16_hi(xw[e >> 1]) : bf16_lo(xw[e >> 1]);
+      if (d != nullptr) {
+        const uint32_t dw[4] = {dv[u].x, dv[u].y, dv[u].z, dv[u].w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t p = pack_bf16x2(v[i][e] + bf16_lo(dw[e >> 1]), v[i][e + 1] + bf16_hi(dw[e >> 1]));
+          ow[e >> 1] = p;
+          v[i][e] = bf16_lo(p);
+          v[i][e + 1] = bf16_hi(p);
+        }
+        *reinterpret_cast<uint4*>(xo + row * xo_stride + 8 * c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+    }
   }
   ss = wave_sum_fixed(ss);
   const float r = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
 #pragma unroll
-  for (int i = 0; i < kRmsChunks; ++i) {
-    const int c = lane + 64 * i;
-    if (c >= chunks) break;
-    const float4 wa = *reinterpret_cast<const float4*>(w1 + 8 * c);
-    const float4 wb = *reinterpret_cast<const float4*>(w1 + 8 * c + 4);
-    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    uint32_t hw[4];
+  for (int i0 = 0; i0 < kRmsChunks; i0 += kRmsGroup) {
+    if (lane + 64 * i0 >= chunks) break;
+    float4 wa[kRmsGroup], wb[kRmsGroup];
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) hw[e >> 1] = pack_bf16x2(v[i][e] * r * wv[e], v[i][e + 1] * r * wv[e + 1]);
-    *reinterpret_cast<uint4*>(h + row * h_stride + 8 * c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    for (int u = 0; u < kRmsGroup; ++u) {
+      const int c = lane + 64 * (i0 + u);
+      if (c < chunks) {
+        wa[u] = *reinterpret_cast<const float4*>(w1 + 8 * c);
+        wb[u] = *reinterpret_cast<const float4*>(w1 + 8 * c + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRmsGroup; ++u) {
+      const int i = i0 + u, c = lane + 64 * i;
+      if (c >= chunks) break;
+      const float wv[8] = {wa[u].x, wa[u].y, wa[u].z, wa[u].w, wb[u].x, wb[u].y, wb[u].z, wb[u].w};
+      uint32_t hw[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) hw[e >> 1] = pack_bf16x2(v[i][e] * r * wv[e], v[i][e + 1] * r * wv[e + 1]);
+      *reinterpret_cast<uint4*>(h + row * h_stride + 8 * c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    }
   }
 }
 
