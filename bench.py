@@ -1,6 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the batched multi-LoRA INT4 linear on one MI355X: tokens/s of a whole pass and the roofline fraction
-of its dominant kernel, with the CPU restatement of the reference's torch layer timed beside it.
+of its dominant kernel, with the CPU restatement of the reference's torch layer timed beside it on every workload,
+and the reference's other product ("cublas": torch's GEMM on the dequantised bf16 weights, then lora_add) timed
+against the INT4 product by the reference's own choice rule.
 
 A step is one pass over one batch: route the request rows by adapter, then every fused group of every layer
 (int4_product: LoRA first factor, then the INT4 base product with the second factor fused; the decoder's gate_up
@@ -13,8 +15,10 @@ as a HIP graph and replayed. Inputs (weights, adapter pool, activations) are res
 The printed line's workload is prefill-skewed-28l (default): 28 layers of hidden 2048 / intermediate 6144, 512
 requests of LogNormal(ln 200, 1) lengths clipped to 16..2048, 128 adapters of rank 32 with Zipf(1.1) popularity, the
 largest single-GPU workload by work. The same run measures decode-28l (256 one-token rows, 64 adapters of ranks
-8..64), decode-pool-28l (4096 one-token rows, 1024 adapters of rank 64, a 142.8 GB pool) and prefill-1layer (one
-1024 -> 3072 layer, 64 requests of 16..256 tokens), each with its own roofline block, under config.workloads.
+8..64), decode-pool-28l (4096 one-token rows, 1024 adapters of rank 64, a 142.8 GB pool), prefill-1layer (one
+1024 -> 3072 layer, 64 requests of 16..256 tokens) and cpu-1024 (the CPU reference configuration: one bf16 1024 ->
+1024 layer, 256 tokens in 8 requests of 32, 4 adapters of rank 16), each with its own roofline block and CPU
+baseline, under config.workloads.
 Progress goes to stderr; stdout holds the one JSON line."""
 
 from __future__ import annotations
@@ -31,7 +35,7 @@ METRIC = "tokens/s for batched multi-LoRA int4 linear; % of HBM/MFMA roofline"
 PEAK_HBM = 8.0e12      # bytes/s, MI355X HBM3E
 PEAK_BF16 = 2.5e15     # flop/s, MI355X dense bf16 MFMA
 HEADLINE = "prefill-skewed-28l"
-ALSO = ("decode-28l", "decode-pool-28l", "prefill-1layer")
+ALSO = ("decode-28l", "decode-pool-28l", "prefill-1layer", "cpu-1024")
 DOMINANT = "gate_up"   # the largest group of every workload: its layer-0 product is the dominant kernel
 EPILOGUE = {"gate_up": "silu_mul"}  # SiLU(gate) * up in the gate_up product's output tile (decoder workloads)
 BOX_THREADS = 16       # the host threads one GPU's share of the machine offers
@@ -46,7 +50,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=HEADLINE)
     ap.add_argument("--also", default=",".join(ALSO), help="other workloads measured in the same run, or 'none'")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-choice", action="store_true",
+                    help="skip timing the library GEMM product (\"cublas\") beside the INT4 product")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on each CPU thread count's timed work")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches of the dominant kernel timed (0: auto)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -116,8 +122,70 @@ def capture(fn, reps: int):
     return g
 
 
-def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool) -> tuple[dict, dict]:
-    """One workload: (its measurements, the objects the CPU baseline needs when `headline`)."""
+def cpu_sample(w, xs: dict) -> dict:
+    """What the CPU baseline of a workload needs, on the host: one layer's groups (the oracle's dequantised weights,
+    or the bf16 W of a bf16 base; the adapters the sample's tokens read) over the pass's first requests up to
+    CPU_SAMPLE_TOKENS tokens (the whole pass when it is smaller)."""
+    import numpy as np
+
+    from jeff_amd import workloads
+    from oracle.pool_view import adapters_of, weights_of
+
+    tok = workloads.token_ids(w)
+    cu = np.concatenate([[0], np.cumsum(w.lengths)])
+    m = int(np.searchsorted(cu, min(CPU_SAMPLE_TOKENS, w.tokens)))
+    t_s = int(cu[m])
+    tok_s = tok[:t_s]
+    pres = sorted({int(a) for a in tok_s})
+    groups = []
+    for label, lin in w.layers[0].items():
+        wt = lin.W.cpu() if lin.int4 is None else weights_of(lin.int4)
+        groups.append((label, xs[(0, label)][:t_s].cpu(), wt, adapters_of(lin, pres), lin.sizes))
+    return {"tok": tok_s, "layers": len(w.layers), "tokens": t_s, "requests": m, "all_tokens": w.tokens,
+            "groups": groups}
+
+
+def product_choice(w, xs: dict, ws, per_layer_acts: bool) -> dict:
+    """The reference's choice between its product kernels for this pass (engine/batched_path.py:492-524 with
+    product_choice.choose_product): every fused group of every layer once, in layer order, plain products (no
+    epilogue), recorded as one graph per candidate and timed in alternating rounds, the median of each kept. "cublas"
+    is Lin.__call__ (torch's GEMM on the dequantised bf16 W, then the HIP lora_add); "int4" is int4_product."""
+    import torch
+
+    from jeff_amd.int4 import dequantize_kernel
+    from jeff_amd.product_choice import choose_product, product
+
+    lins = [(li, label, lin) for li, layer in enumerate(w.layers) for label, lin in layer.items()]
+    for _, _, lin in lins:
+        lin.W = dequantize_kernel(lin.int4)
+    stream = torch.cuda.current_stream()
+    graphs = {}
+
+    def time_ms(kernel: str) -> float:
+        if kernel not in graphs:
+            prod = product(kernel)
+
+            def products() -> None:
+                for li, label, lin in lins:
+                    prod(lin, xs[(li if per_layer_acts else 0, label)], ws, w.adp)
+
+            graphs[kernel] = capture(products, 1)
+        return replay_ms(graphs[kernel], stream, 1, rounds=1)
+
+    pick = choose_product(("cublas", "int4"), time_ms)
+    graphs.clear()
+    for _, _, lin in lins:
+        lin.W = None
+    torch.cuda.empty_cache()
+    note(f"{w.name}: product choice {pick.kernel} {pick.ms}")
+    return {"kernel": pick.kernel, "ms_per_pass": pick.ms,
+            "note": "the reference's rule: every group of every layer once per candidate, medians of 3 alternating "
+                    "rounds, the faster recorded (cublas: torch GEMM on the dequantised bf16 W + HIP lora_add)"}
+
+
+def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool, want_cpu: bool = True,
+            compare_products: bool = True) -> tuple[dict, dict]:
+    """One workload: (its measurements, the objects its CPU baseline needs)."""
     import torch
 
     from jeff_amd import workloads
@@ -140,11 +208,14 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
             if per_layer_acts or li == 0:
                 xs[(li, label)] = workloads.inputs(w, label, gen)
     max_rank = max(lin.rank for layer in w.layers for lin in layer.values())
-    ws = Workspace(w.tokens, 1, max_rank=max_rank, max_requests=w.requests)
+    shapes = {(lin.k, lin.out) for layer in w.layers for lin in layer.values()}
+    ws = Workspace(w.tokens, 1, shapes, max_rank=max_rank, max_requests=w.requests)
     last = torch.empty(w.requests, w.layers[-1]["down"].out, dtype=DT, device=dev) if w.gather_last else None
     keep: list[torch.Tensor] = []
     torch.cuda.synchronize()
     note(f"{name}: built in {time.perf_counter() - t_build:.1f} s ({w.tokens} tokens, {len(w.layers)} layers)")
+
+    bf16_base = all(lin.int4 is None for layer in w.layers for lin in layer.values())
 
     def step() -> None:
         ws.route(w.adp, pool_rows, tokens=w.tokens, cu_seqlens=w.cu_seqlens)
@@ -152,6 +223,9 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
         for li, layer in enumerate(w.layers):
             for label, lin in layer.items():
                 x = xs[(li if per_layer_acts else 0, label)]
+                if bf16_base:  # the reference's "cublas" product: torch's GEMM on W, then lora_add
+                    keep.append(lin(x, ws, w.adp))
+                    continue
                 gather = last if (last is not None and li == len(w.layers) - 1 and label == "down") else None
                 epi = EPILOGUE.get(label) if w.gated else None
                 keep.append(int4_product(lin, x, ws, w.adp, last_out=gather, epilogue=epi))
@@ -183,6 +257,31 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
     tokens_per_s = w.tokens / (ms_per_step / 1e3)
     note(f"{name}: {steps} steps of {ms_per_step:.3f} ms")
     del graph
+    cpu_inputs = cpu_sample(w, xs) if want_cpu else {}
+    step_flops = workloads.flops_per_token(w) * w.tokens
+    step_bytes = workloads.hbm_bytes(w, gated=tuple(EPILOGUE) if w.gated else ())
+    step_roof = {"mfma_frac": step_flops / (ms_per_step / 1e3) / PEAK_BF16,
+                 "hbm_frac": step_bytes / (ms_per_step / 1e3) / PEAK_HBM,
+                 "flops": step_flops, "bytes": step_bytes}
+    if bf16_base:
+        # one bf16 layer: the step is the whole product (x W^T on torch's GEMM, then the HIP lora_add), so the step's
+        # time is the product's; launch-bound at this size
+        result = {"workload": name, "value": tokens_per_s, "unit": "tokens/s", "ms_per_step": ms_per_step,
+                  "steps": steps, "warmup": warmup, "tokens": w.tokens, "requests": w.requests,
+                  "layers": len(w.layers), "groups": {k: [v.k, v.out] for k, v in w.layers[0].items()},
+                  "adapters": len(w.adapter_ranks), "ranks": sorted(set(w.adapter_ranks.values())),
+                  "base": "bf16 (torch GEMM on W, then mlora_lora_add: the reference's Lin.__call__)",
+                  "roofline": {"bound": "mfma", "achieved": step_flops / (ms_per_step / 1e3) / 1e12,
+                               "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                               "frac": step_flops / (ms_per_step / 1e3) / PEAK_BF16, "traffic": None,
+                               "kernel": "torch GEMM + lora_add (shrink_seg_kernel, base_mfma_kernel<false>)",
+                               "note": "launch-bound: 0.55 GFLOP per step"},
+                  "step_roofline": step_roof}
+        del w, xs, keep, ws, last
+        gc.collect()
+        torch.cuda.empty_cache()
+        return result, cpu_inputs
+    choice = product_choice(w, xs, ws, per_layer_acts) if compare_products else None
 
     # the dominant kernel alone: the base product and the LoRA second factor of layer 0's gate_up (one launch of the
     # fused 256-tile kernel for prefill; for decode the narrow or split product's launches), timed with HIP events on
@@ -238,21 +337,16 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
                        f"{'finish_gated_kernel' if gated else 'finish_kernel'} (INT4 base + LoRA expand{fin})",
               "narrow": f"dec_kernel (INT4 base + fused LoRA expand{fin}; {ranges} input ranges"
                         + (", added by dec_reduce_kernel)" if ranges > 1 else ")"),
-              "rowtile": f"rowtile_kernel<{ranges}> (INT4 base + LoRA expand streamed with the input loop{fin}; "
-                         f"64 sorted rows x {64 * ranges} columns per workgroup)",
               "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[base]
     roof.update({"kernel": kernel, "group": f"layer0.{DOMINANT}", "launch_ms": kms, "reps": reps,
                  "route_ms_subtracted": route_ms, "flops_per_launch": kflops, "bytes_per_launch": kbytes})
-    step_flops = workloads.flops_per_token(w) * w.tokens
-    step_bytes = workloads.hbm_bytes(w, gated=tuple(EPILOGUE) if w.gated else ())
-    step_roof = {"mfma_frac": step_flops / (ms_per_step / 1e3) / PEAK_BF16,
-                 "hbm_frac": step_bytes / (ms_per_step / 1e3) / PEAK_HBM,
-                 "flops": step_flops, "bytes": step_bytes}
     result = {"workload": name, "value": tokens_per_s, "unit": "tokens/s", "ms_per_step": ms_per_step,
               "steps": steps, "warmup": warmup, "tokens": w.tokens, "requests": w.requests, "layers": len(w.layers),
               "groups": {k: [v.k, v.out] for k, v in w.layers[0].items()},
               "adapters": len(w.adapter_ranks), "ranks": sorted(set(w.adapter_ranks.values())),
               "group_size": 128, "zero_points": True, "roofline": roof, "step_roofline": step_roof}
+    if choice is not None:
+        result["product_choice"] = choice
     note(f"{name}: dominant kernel {kms:.4f} ms, {roof['frac']:.3f} of the {roof['bound']} roofline")
 
     if gated:
@@ -363,20 +457,6 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
                                "silu_mul": timed(lambda: silu_mul(egu), 2.0 * w.tokens * inter * 3)}
         del ex, ed, egu
 
-    cpu_inputs = {}
-    if headline:  # what the CPU baseline needs, on the host: the pass's first requests, about CPU_SAMPLE_TOKENS
-        import numpy as np
-
-        from oracle.pool_view import adapters_of, weights_of
-        cu = np.concatenate([[0], np.cumsum(w.lengths)])
-        m = int(np.searchsorted(cu, min(CPU_SAMPLE_TOKENS, w.tokens)))
-        t_s = int(cu[m])
-        tok_s = tok[:t_s]
-        pres = sorted({int(a) for a in tok_s})
-        cpu_inputs = {"tok": tok_s, "layers": len(w.layers), "tokens": t_s, "requests": m,
-                      "all_tokens": w.tokens,
-                      "groups": [(label, xs[(0, label)][:t_s].cpu(), weights_of(l.int4), adapters_of(l, pres), l.sizes)
-                                 for label, l in w.layers[0].items()]}
     del w, xs, keep, ws, last, y, x, lin
     gc.collect()
     torch.cuda.empty_cache()
@@ -392,6 +472,27 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def lscpu() -> dict:
+    """The host's lscpu fields that say what the CPU baseline ran on (empty when lscpu is missing)."""
+    import subprocess
+    keep = ("Model name", "Vendor ID", "CPU(s)", "On-line CPU(s) list", "Thread(s) per core", "Core(s) per socket",
+            "Socket(s)", "NUMA node(s)", "CPU max MHz", "L3 cache", "Flags")
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return {}
+    info = {}
+    for line in out.splitlines():
+        key, _, val = line.partition(":")
+        key = key.strip()
+        if key in keep:
+            val = val.strip()
+            if key == "Flags":  # the vector extensions torch's CPU GEMM can use
+                val = " ".join(f for f in val.split() if f.startswith(("avx512", "avx2", "amx", "fma")))
+            info[key] = val
+    return info
 
 
 def cpu_baseline(inp: dict, budget_s: float) -> dict:
@@ -432,13 +533,20 @@ def cpu_baseline(inp: dict, budget_s: float) -> dict:
     scale = inp["layers"]
     tokens = inp["tokens"]
     labels = ", ".join(g[0] for g in inp["groups"])
+    whole = tokens == inp["all_tokens"]
+    what = (f"the whole pass ({tokens} tokens in {inp['requests']} requests)" if whole else
+            f"the pass's first {inp['requests']} requests ({tokens} of its {inp['all_tokens']} tokens)")
+    if scale == 1:
+        sample = f"{labels} over {what}, bf16 torch on the CPU, median of {runs} runs after 3 warm-ups"
+    else:
+        sample = (f"one layer of {scale} ({labels}) over {what}, bf16 torch on the CPU, median of {runs} runs after 3 "
+                  f"warm-ups; tokens/s scaled by 1/{scale} for the whole pass (an extrapolation: the {scale} layers "
+                  f"have the same shapes)")
     return {"value": tokens / (per_layer * scale), "unit": "tokens/s", "cores": share, "kind": "port",
-            "sample": f"one layer of {scale} ({labels}) over the pass's first {inp['requests']} requests "
-                      f"({tokens} of its {inp['all_tokens']} tokens), bf16 torch on the CPU, median of {runs} runs "
-                      f"after 3 warm-ups; tokens/s scaled by 1/{scale} for the whole pass (an extrapolation)",
-            "per_layer_s": per_layer, "threads_8": {"value": tokens / (per_layer8 * scale), "cores": 8,
-                                                    "per_layer_s": per_layer8, "runs": runs8},
-            "host_cpus": host, "cpu_model": cpu_model()}
+            "sample": sample, "per_layer_s": per_layer,
+            "threads_8": {"value": tokens / (per_layer8 * scale), "cores": min(REFERENCE_THREADS, host),
+                          "per_layer_s": per_layer8, "runs": runs8},
+            "host_cpus": host, "cpu_model": cpu_model(), "lscpu": lscpu()}
 
 
 def main() -> int:
@@ -453,11 +561,19 @@ def main() -> int:
     import torch
     torch.cuda.set_device(0)
     also = [] if args.also in ("", "none") else [n for n in args.also.split(",") if n != args.workload]
-    head, cpu_inputs = measure(args.workload, args.steps, args.warmup, args.kernel_reps, headline=True)
-    others = {}
+    want_cpu = not args.no_cpu
+    head, cpu_inputs = measure(args.workload, args.steps, args.warmup, args.kernel_reps, headline=True,
+                               want_cpu=want_cpu, compare_products=not args.no_choice)
+    others, other_inputs = {}, {}
     for name in also:
-        others[name], _ = measure(name, args.steps, args.warmup, args.kernel_reps, headline=False)
-    cpu = None if args.no_cpu else cpu_baseline(cpu_inputs, args.cpu_seconds)
+        others[name], other_inputs[name] = measure(name, args.steps, args.warmup, args.kernel_reps, headline=False,
+                                                   want_cpu=want_cpu, compare_products=not args.no_choice)
+    # the CPU baselines after every GPU measurement, so host work never overlaps the GPU's timed regions
+    cpu = cpu_baseline(cpu_inputs, args.cpu_seconds) if want_cpu else None
+    for name, inp in other_inputs.items():
+        if inp:
+            others[name]["cpu_baseline"] = cpu_baseline(inp, args.cpu_seconds)
+            other_inputs[name] = None
     config = {k: v for k, v in head.items() if k not in ("value", "unit", "ms_per_step", "steps", "warmup",
                                                          "roofline")}
     config["workloads"] = others

@@ -23,6 +23,7 @@
  *   mlora_int4_plan    int4_tiles (the tile and kernel choice of a shape)   int4_tiles.py:57-71
  *   mlora_workspace_bytes  Workspace.QP sizing                             fast_path.py:261-274
  *   mlora_int4_partials_bytes  Workspace.P sizing (split partial products)  int4_kernels.py:150-166
+ *   mlora_int4_partials_bound  Workspace sizing from its shapes up front     fast_path.py:261-274
  *   mlora_readout_logits  readout_logits (per-adapter readout)          batched_kernels.py:492-504,522-536
  *   mlora_option_softmax  option_softmax (mask, temperature, softmax)     batched_kernels.py:507-519,539-553
  *   mlora_add_rms      add_rms / rms (residual add + RMSNorm)              fast_path.py:80-100,295-298
@@ -73,10 +74,6 @@ enum {
 #define MLORA_FORCE_BASE_SPLIT 16   /* split product: float32 partials, then a per-segment epilogue launch */
 #define MLORA_FORCE_BASE_NARROW 32  /* narrow product (at most 256 tokens): every token in one row tile of 64 columns */
 #define MLORA_FORCE_RANGES(s) ((s) << 8)  /* a narrow product over s = 1, 2, 4 or 8 input ranges (s dividing k / 64) */
-/* row-tile product: 64 sorted rows x 64, 128 or 192 columns per workgroup, the LoRA second factor streamed with the
- * input loop; group matrices whose widths are multiples of 16 (gated: gate and up widths multiples of 32) and rank
- * capacities of at most 64 */
-#define MLORA_FORCE_BASE_ROWTILE 4096
 /* Epilogue flag: the group is a gate_up pair (matrix 0 gate, matrix 1 up, out / 2 columns each, out a multiple of
  * 256, one rank capacity of at most 64 for both); y (and last_out) receive silu(gate) * up, out / 2 columns per row,
  * each element
@@ -193,6 +190,13 @@ size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora
  * x_stride elements apart (k a multiple of 64, rows 16-byte aligned). last_out (requests, w->out) bf16 or NULL:
  * each request's last-token output row as well. workspace: the first factors (mlora_workspace_bytes);
  * partials: mlora_int4_partials_bytes of float32 scratch (NULL when that is 0). */
+/* The most float32 partial bytes any product of a group of k inputs, `columns` kernel columns and `out` outputs over
+ * at most `tokens` tokens needs under the automatic kernel choice (any request count, pool, epilogue or x stride),
+ * so a workspace can be sized once from its shapes, before any pass is recorded (host only, no GPU needed; the
+ * narrow range count follows the current device's CU count, 256 without a device). 0 for arguments no product
+ * accepts. Forced kernel flags (tests) can need more: mlora_int4_partials_bytes says how much. */
+size_t mlora_int4_partials_bound(int32_t k, int32_t columns, int32_t out, int64_t tokens);
+
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
                       const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out,
                       void* workspace, size_t workspace_bytes, void* partials, size_t partials_bytes, int32_t flags,
@@ -201,9 +205,10 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
 /* mlora_int4_linear with its scratch inside the library: no counterpart in the reference, for callers that cannot
  * allocate device memory or pass a workspace (code under graph capture that must not allocate, tight serving loops,
  * harnesses that forbid hipMalloc). The first factors and any float32 partials live in a static device array of
- * MLORA_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU until the process ends; the call
- * allocates nothing and returns MLORA_EWORKSPACE before any launch when a pass needs more (mlora_workspace_bytes +
- * mlora_int4_partials_bytes). Every call on one GPU shares that GPU's array and leaves its contents behind; the
+ * MLORA_NOALLOC_SCRATCH_BYTES in the library's code object: every GPU on which the library's kernels are loaded
+ * holds its own copy from then until the process ends, whether or not this entry point is called. The call
+ * allocates nothing and returns MLORA_EWORKSPACE before any launch when a pass needs more (mlora_workspace_bytes
+ * plus the partials of the kernels chosen for this call's x_stride). Every call on one GPU shares that GPU's array and leaves its contents behind; the
  * kernels write every scratch byte they read, so nothing needs clearing, but calls that overlap on one GPU (other
  * streams, other threads) race on it. Same arguments, results and bits as mlora_int4_linear otherwise. */
 int mlora_int4_linear_noalloc(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
@@ -244,8 +249,9 @@ int mlora_add_rms(const uint16_t* x, int64_t x_stride, const uint16_t* d, int64_
                   void* stream);
 
 /* The gated activation after the gate_up product (the reference's silu_mul): for each of `rows` rows of gu (the
- * gate half in columns 0..inter-1, the up half in inter..2 inter-1), y = bf16(bf16(g / (1 + exp(-g))) * u). inter a
- * multiple of 8; rows 16-byte aligned, strides multiples of 8 elements. */
+ * gate half in columns 0..inter-1, the up half in inter..2 inter-1), y = bf16(bf16(g / (1 + exp(-g))) * u), the
+ * quotient correctly rounded to float32 (signed zeros, infinities and NaN as the float32 formula gives them). inter
+ * a multiple of 8; rows 16-byte aligned, strides multiples of 8 elements. */
 int mlora_silu_mul(const uint16_t* gu, int64_t gu_stride, uint16_t* y, int64_t y_stride, int64_t rows, int32_t inter,
                    void* stream);
 

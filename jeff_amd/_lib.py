@@ -30,7 +30,6 @@ ROUTE_BAD_ADAPTER = 1
 ROUTE_BAD_SEQLENS = 2
 FORCE_BASE_GEMV, FORCE_BASE_MFMA, FORCE_SHRINK_SEGMENT, FORCE_SHRINK_MFMA, FORCE_BASE_SPLIT = 1, 2, 4, 8, 16
 FORCE_BASE_NARROW = 32
-FORCE_BASE_ROWTILE = 4096
 EPILOGUE_SILU_MUL = 64
 EPILOGUE_RESIDUAL = 128
 
@@ -41,7 +40,7 @@ def force_ranges(s: int) -> int:
 
 
 EXPORTS = ("mlora_abi_version", "mlora_capture_id", "mlora_workspace_bytes", "mlora_int4_partials_bytes",
-           "mlora_route", "mlora_dequant", "mlora_int4_plan", "mlora_shrink", "mlora_int4_linear",
+           "mlora_int4_partials_bound", "mlora_route", "mlora_dequant", "mlora_int4_plan", "mlora_shrink", "mlora_int4_linear",
            "mlora_int4_linear_noalloc", "mlora_int4_base_expand", "mlora_lora_add", "mlora_readout_logits",
            "mlora_option_softmax", "mlora_add_rms", "mlora_silu_mul")
 
@@ -124,6 +123,8 @@ def lib() -> ctypes.CDLL:
         h.mlora_silu_mul.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_i32, c_vp]
         h.mlora_int4_partials_bytes.restype = ctypes.c_size_t
         h.mlora_int4_partials_bytes.argtypes = [P(Int4), P(Lora), P(Route), c_i32]
+        h.mlora_int4_partials_bound.restype = ctypes.c_size_t
+        h.mlora_int4_partials_bound.argtypes = [c_i32, c_i32, c_i32, c_i64]
         h.mlora_lora_add.restype = c_i32
         h.mlora_lora_add.argtypes = [P(Lora), P(Route), c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_vp,
                                      ctypes.c_size_t, c_i32, c_vp]

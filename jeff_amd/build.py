@@ -17,7 +17,7 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = ROOT / "include"
 OBJ_DIR = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libjeff_mlora.so"
-SOURCES = ("route.hip", "shrink.hip", "base.hip", "gemm256.hip", "decode.hip", "rowtile.hip", "finish.hip", "readout.hip",
+SOURCES = ("route.hip", "shrink.hip", "base.hip", "gemm256.hip", "decode.hip", "finish.hip", "readout.hip",
            "epilogue.hip", "api.hip")
 ARCH = "gfx950"
 

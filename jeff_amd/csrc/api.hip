@@ -82,7 +82,7 @@ bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
   return long_segments(r, pool_rows);
 }
 
-enum class Base { gemv, fused, split, narrow, rowtile };
+enum class Base { gemv, fused, split, narrow };
 
 constexpr int64_t kNarrowMaxTokens = 256;  // the narrow kernel's row tile holds every token of the pass
 
@@ -113,16 +113,6 @@ int device_cus() {
   return cus[dev];
 }
 
-// The row-tile product runs this group: column blocks for its widths and capacities, 32-bit x offsets.
-int rowtile_nb(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int32_t flags) {
-  return rowtile_blocks(*w, *L, r->tokens > 0 ? r->tokens : 1, gated_width(w, flags), device_cus());
-}
-bool rowtile_fits(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride,
-                  int32_t flags) {
-  const int64_t row = x_stride > w->k ? x_stride : w->k;
-  return rowtile_nb(w, L, r, flags) > 0 && (r->tokens == 0 || row < ((int64_t)1 << 31) / r->tokens);
-}
-
 int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, int64_t x_stride, int32_t flags,
             Base* out) {
   const bool gated = (flags & MLORA_EPILOGUE_SILU_MUL) != 0, resid = residual_of(flags);
@@ -138,16 +128,13 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
   } else if (flags & MLORA_FORCE_BASE_NARROW) {
     if (r->tokens > kNarrowMaxTokens || !split_fits(w, L, r, x_stride)) return MLORA_EUNSUPPORTED;
     *out = Base::narrow;
-  } else if (flags & MLORA_FORCE_BASE_ROWTILE) {
-    if (!rowtile_fits(w, L, r, x_stride, flags)) return MLORA_EUNSUPPORTED;
-    *out = Base::rowtile;
   } else if (flags & MLORA_FORCE_BASE_MFMA) {
     *out = Base::fused;
   } else if (r->tokens <= 8 && !gated && !resid) {  // (the GEMV kernel has no epilogues: few tokens take the tiles)
     *out = Base::gemv;
   } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
     *out = Base::fused;
-  } else {  // (the row-tile product runs when forced: on the decode shapes it is not yet faster than these)
+  } else {
     *out = r->tokens <= kNarrowMaxTokens ? Base::narrow : Base::split;
   }
   if (fs != 0 && *out != Base::narrow) return MLORA_EUNSUPPORTED;
@@ -211,15 +198,18 @@ size_t split_bytes(const mlora_int4_t* w, int64_t tokens) {
   return ((size_t)split_ranges(w, tokens) * (size_t)tokens * (size_t)w->columns * 4 + 255) & ~(size_t)255;
 }
 
+// Float32 partial bytes the base kernels `base` read and write for this product (0 for the fused kernels).
+size_t partials_of(const mlora_int4_t* w, const mlora_route_t* r, Base base, int32_t flags) {
+  if (base == Base::narrow) return dec_partials_bytes(*w, narrow_ranges(w, flags));
+  return base == Base::split ? split_bytes(w, r->tokens) : 0;
+}
+
 // The base product (and the LoRA second factor) once mid holds the first factors.
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
              int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
              void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
   const int32_t inter = gated_width(w, flags);
   const bool resid = residual_of(flags);
-  if (base == Base::rowtile)
-    return launch_rowtile(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, rowtile_nb(w, L, r, flags), s,
-                          inter, resid);
   if (base == Base::narrow) {
     const int32_t ks = narrow_ranges(w, flags);
     const size_t need = dec_partials_bytes(*w, ks);
@@ -317,10 +307,9 @@ int mlora_int4_plan(int32_t k, int32_t columns, int32_t out, int64_t tokens, int
   Base b;
   const int rc = base_of(&w, &L, &r, k, flags, &b);
   if (rc) return rc;
-  *base = b == Base::gemv ? 0 : b == Base::fused ? 1 : b == Base::split ? 2 : b == Base::narrow ? 3 : 4;
+  *base = b == Base::gemv ? 0 : b == Base::fused ? 1 : b == Base::split ? 2 : 3;
   *shrink = shrink_on_mfma(&r, pool_rows, flags) ? 1 : 0;
-  *ranges = b == Base::narrow ? narrow_ranges(&w, flags) : b == Base::split ? split_ranges(&w, tokens)
-            : b == Base::rowtile ? rowtile_nb(&w, &L, &r, flags) : 1;
+  *ranges = b == Base::narrow ? narrow_ranges(&w, flags) : b == Base::split ? split_ranges(&w, tokens) : 1;
   return MLORA_OK;
 }
 
@@ -352,8 +341,30 @@ size_t mlora_int4_partials_bytes(const mlora_int4_t* w, const mlora_lora_t* lora
   if (check_int4(w) || check_route(route) || check_lora(lora, w->k, w->out) || route->tokens == 0) return 0;
   Base base;
   if (base_of(w, lora, route, w->k, flags, &base)) return 0;
-  if (base == Base::narrow) return dec_partials_bytes(*w, narrow_ranges(w, flags));
-  return base == Base::split ? split_bytes(w, route->tokens) : 0;
+  return partials_of(w, route, base, flags);
+}
+
+size_t mlora_int4_partials_bound(int32_t k, int32_t columns, int32_t out, int64_t tokens) {
+  if (k <= 0 || k % 64 || columns <= 0 || columns % 64 || out <= 0 || out > columns || tokens <= 0 ||
+      tokens >= INT_MAX)
+    return 0;
+  const mlora_int4_t w = {nullptr, nullptr, nullptr, k, columns, out, 64};
+  // a narrow product (at most kNarrowMaxTokens tokens) at the automatic range count
+  size_t most = dec_partials_bytes(w, narrow_ranges(&w, 0));
+  // a split product of t <= tokens tokens (more than kNarrowMaxTokens unless forced): within each 256-token band of
+  // row tiles the range count is fixed, so the band's last token count needs the most; once a band runs one range
+  // the bytes only grow with t, so the last is `tokens` itself
+  for (int64_t m = 1; 256 * (m - 1) < tokens; ++m) {
+    const int64_t t = 256 * m < tokens ? 256 * m : tokens;
+    const size_t b = split_bytes(&w, t);
+    most = b > most ? b : most;
+    if (split_ranges(&w, t) == 1) {
+      const size_t last = split_bytes(&w, tokens);
+      most = last > most ? last : most;
+      break;
+    }
+  }
+  return most;
 }
 
 int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
@@ -413,7 +424,7 @@ int mlora_int4_linear_noalloc(const mlora_int4_t* w, const mlora_lora_t* lora, c
   Base base;
   if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
   const size_t first = mlora_workspace_bytes(route->tokens, lora->rank_cap);  // a multiple of 256
-  const size_t part = mlora_int4_partials_bytes(w, lora, route, flags);
+  const size_t part = partials_of(w, route, base, flags);  // of the kernels this launch (its x_stride) runs
   if (first > MLORA_NOALLOC_SCRATCH_BYTES || part > MLORA_NOALLOC_SCRATCH_BYTES - first) return MLORA_EWORKSPACE;
   uint8_t* sp = noalloc_scratch();
   if (sp == nullptr) return MLORA_ELAUNCH;

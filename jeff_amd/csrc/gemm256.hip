@@ -282,9 +282,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
   // set to zero. The first two segments' adapters and live ranks of the first matrix were read in the prologue.
   if constexpr (GATED) {
-    // Gated: gate and up have one capacity c <= 64 (the host checks it), so their stacked ranks [0, 2c) are staged at
-    // once ([0, 64) in the first buffer, [64, 128) in the second) and each wave adds only its own matrix's term
-    // (waves 0..3 gate, waves 4..7 up).
+    // Gated: gate and up have one capacity c <= 64 (the host checks it), so both matrices' first factors are staged
+    // at once and each wave adds only its own matrix's term (waves 0..3 gate, waves 4..7 up). When 2c <= 64 the
+    // stacked ranks [0, 2c) fit the first buffer (up's from chunk c / 8); otherwise the first buffer holds stacked
+    // ranks [0, 64) (gate's c ranks first) and the second stacked ranks [c, c + 64) (up's, from chunk 0). Ranks past a
+    // matrix's own c are the other matrix's or the next row's; they are masked by the live rank.
     if (lora) {
       const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
           (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
@@ -298,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         for (int i = 0; i < kXLoads; ++i) {
           const int row = (8 * i + wave) * 8 + (lane >> 3);
           const uint32_t off =
-              (uint32_t)(((p0 + row) * L.rank_cap + h * kRankChunk + (swz_slot(row, lane & 7) << 3)) * 2);
+              (uint32_t)(((p0 + row) * L.rank_cap + h * L.cap[0] + (swz_slot(row, lane & 7) << 3)) * 2);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)((h ? g_x1 : g_x0) + (8 * i + wave) * 8 * kTK),
                                                    16, off, 0, 0, 0);
         }

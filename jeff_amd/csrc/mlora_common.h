@@ -74,7 +74,8 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_ca
 // q0 + residual rcp(d), rounded once, is the correctly rounded quotient except within about 2^-22 ulp of a rounding
 // boundary (a bare reciprocal, within 1 ulp, misrounds values within an ulp of a bf16 rounding midpoint). Where d
 // reaches 2^120 (g below about -83: the reciprocal would fall among the denormals, which it flushes) the quotient is
-// an IEEE division.
+// an IEEE division. Where q0 is a zero, an infinity or NaN (g = +-0, +inf, NaN) q0 itself is the quotient: the
+// correction step would turn -0 into +0 and +inf into NaN.
 __device__ __forceinline__ float bf16_round(float v) {
   return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v) << 16);
 }
@@ -83,7 +84,9 @@ __device__ __forceinline__ float silu_quotient(float g) {
   if (__builtin_expect(!(d < 0x1p120f), 0)) return g / d;
   const float r = __builtin_amdgcn_rcpf(d);
   const float q0 = g * r;
-  return __builtin_fmaf(__builtin_fmaf(-q0, d, g), r, q0);
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, d, g), r, q0);
+  // classes: signalling/quiet NaN (bits 0, 1), -inf (2), -0 (5), +0 (6), +inf (9)
+  return __builtin_amdgcn_class(q0, 0x3 | 0x4 | 0x20 | 0x40 | 0x200) ? q0 : q;
 }
 __device__ __forceinline__ uint4 silu_mul8(uint4 g, uint4 u) {
   const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
@@ -244,13 +247,6 @@ int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t
                int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
                bool residual = false);
-// Row-tile product (64 sorted rows x 64 nb columns per workgroup, the LoRA second factor streamed with the K loop):
-// the column blocks per wave for this group (0: the kernel cannot run it), and the launch (residual as above, not
-// gated).
-int rowtile_blocks(const mlora_int4_t& w, const mlora_lora_t& L, int64_t tokens, int32_t inter, int cus);
-int launch_rowtile(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
-                   int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-                   const uint16_t* mid, int nb, hipStream_t stream, int32_t inter = 0, bool residual = false);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                 const uint16_t* mid, bool gemv, hipStream_t stream);

@@ -195,8 +195,10 @@ def reusable(last: RouteRecord, adp: torch.Tensor, tokens: int, pool_rows: int, 
 class Workspace:
     """fast_path.py:261-274: scratch shared by the products of passes of up to `rows` tokens in request rows of
     `row_len` tokens (uniform rows, as the reference's passes), or ragged rows routed with cu_seqlens.
-    `shapes`: the (k, out) of the groups that will run (kept for the reference's interface); `max_rank`: the largest
-    stacked rank capacity (Lin.rank) of those groups; `max_requests`: request rows per pass (default rows/row_len)."""
+    `shapes`: the (k, out) of the groups that will run: the float32 partials of their split and narrow products are
+    allocated here, up front, at the most any of them needs for up to `rows` tokens (mlora_int4_partials_bound), as
+    the reference sizes its QP from the shapes; `max_rank`: the largest stacked rank capacity (Lin.rank) of those
+    groups; `max_requests`: request rows per pass (default rows/row_len)."""
 
     def __init__(self, rows: int, row_len: int, shapes: set[tuple[int, int]] | None = None, *, max_rank: int = 256,
                  max_requests: int | None = None, device: torch.device | str = "cuda") -> None:
@@ -227,15 +229,23 @@ class Workspace:
         self._last: RouteRecord | None = None
         self._route_abi: _lib.Route | None = None
         self._part: torch.Tensor | None = None
+        self._retired: list[torch.Tensor] = []
+        bound = max((h.mlora_int4_partials_bound(k, -(-out // 64) * 64, out, rows) for k, out in self.shapes),
+                    default=0)
+        if bound:
+            self._part = torch.empty(bound, dtype=torch.uint8, device=dev)
 
     def partials(self, nbytes: int) -> tuple[int, int]:
-        """(pointer, bytes) of device scratch for a split product's float32 partial sums, at least nbytes (0: none
-        needed). Grown when a larger product comes and kept, like the reference's Workspace.P
-        (engine/int4_kernels.py:150-166)."""
+        """(pointer, bytes) of device scratch for a split or narrow product's float32 partial sums, at least nbytes
+        (0: none needed). The buffer sized from `shapes` serves every product of those shapes; a product that needs more
+        (a shape not named, or kernels forced by flags) gets a larger buffer, and the smaller one is kept alive with the
+        workspace, never freed: a graph recorded earlier holds its address and writes it on every replay (the reference
+        allocates its partials per product instead, engine/int4_kernels.py:160-166)."""
         if nbytes == 0:
             return 0, 0
         if self._part is None or self._part.numel() < nbytes:
-            self._part = None
+            if self._part is not None:
+                self._retired.append(self._part)
             self._part = torch.empty(nbytes, dtype=torch.uint8, device=self.mid.device)
         return self._part.data_ptr(), self._part.numel()
 

@@ -6,11 +6,9 @@ call that needs no GPU, so the kernel a benchmark names is the one the product r
 - base: "gemv" (at most 8 tokens: one pass over the weights, every token dotted with each dequantised word), "mfma"
   (32x32x16 bf16 MFMA tiles, the LoRA second factor fused into the epilogue), "narrow" (few tokens per adapter
   segment and at most 256 tokens: one row tile of every token by 64 columns, the second factor fused, the input
-  dimension split into float32 ranges only when the columns are too few for the CUs), "split" (few tokens per
+  dimension split into float32 ranges only when the columns are too few for the CUs) or "split" (few tokens per
   segment, more tokens: MFMA tiles over ranges of the input dimension into float32 partials, then one epilogue
-  workgroup per adapter segment and 256 columns) or "rowtile" (few tokens per segment, any number of tokens: 64
-  sorted rows by 64, 128 or 192 columns per workgroup on 16x16x32 MFMAs, each segment's second factor loaded with the
-  input loop's steps and added in the same accumulators).
+  workgroup per adapter segment and 256 columns).
 - shrink (the LoRA first factor): "segment" when segments are short on average (decode: one workgroup per segment
   and 32 ranks of its adapter's A, the segment's rows as the second MFMA operand) or "mfma" when they are long
   (prefill: 32 sorted rows per workgroup on MFMA)."""
@@ -22,7 +20,7 @@ from dataclasses import dataclass
 
 from jeff_amd import _lib
 
-BASES = ("gemv", "mfma", "split", "narrow", "rowtile")  # in the library's numbering (mlora_int4_plan *base)
+BASES = ("gemv", "mfma", "split", "narrow")  # in the library's numbering (mlora_int4_plan *base)
 SHRINKS = ("segment", "mfma")
 
 
@@ -34,7 +32,7 @@ class Int4Tiles:
 
     def flags(self) -> int:
         f = {"gemv": _lib.FORCE_BASE_GEMV, "mfma": _lib.FORCE_BASE_MFMA, "narrow": _lib.FORCE_BASE_NARROW,
-             "split": _lib.FORCE_BASE_SPLIT, "rowtile": _lib.FORCE_BASE_ROWTILE}[self.base]
+             "split": _lib.FORCE_BASE_SPLIT}[self.base]
         f |= 0 if self.ranges is None else _lib.force_ranges(self.ranges)
         return f | (_lib.FORCE_SHRINK_SEGMENT if self.shrink == "segment" else _lib.FORCE_SHRINK_MFMA)
 

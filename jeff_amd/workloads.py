@@ -99,7 +99,18 @@ def make(name: str, device: str = "cuda", seed: int = 0, n_layers: int | None = 
     """Build a workload on `device`. n_layers overrides the 28 layers of the decoder workloads (tests use fewer)."""
     gen = torch.Generator(device=device).manual_seed(seed)
     rng = np.random.default_rng(seed)
-    if name == "prefill-1layer":
+    if name == "cpu-1024":
+        # one bf16 layer (no INT4 weights: the reference's "cublas" product, x W^T then lora_add), W ~ N(0, 0.02)
+        w16 = (0.02 * torch.randn(1024, 1024, generator=gen, device=device)).to(DT)
+        lin = Lin(["layers.0.self_attn.o_proj"], [w16], ranks=[16])
+        pool = AdapterPool([lin], 4, device)
+        ranks = {a: 16 for a in range(1, 5)}
+        _fill_adapters(pool, ranks, gen, device)
+        lengths = np.full(8, 32, dtype=np.int64)
+        ids = rng.integers(1, 5, 8)
+        layers = [{"o": lin}]
+        gather = False
+    elif name == "prefill-1layer":
         lin = Lin(["layers.0.mlp.gate_proj"], sizes=[3072], k=1024, ranks=[16])
         lin.int4 = _int4_weights(3072, 1024, gen, device)
         pool = AdapterPool([lin], 16, device)
@@ -148,7 +159,7 @@ def make(name: str, device: str = "cuda", seed: int = 0, n_layers: int | None = 
                     adp=torch.tensor(ids.astype(np.int32), device=device),
                     cu_seqlens=torch.tensor(cu, device=device) if ragged else None,
                     tokens=int(cu[-1]), requests=len(lengths), lengths=lengths, adapter_ranks=ranks,
-                    gather_last=gather, readout=readout, gated=name != "prefill-1layer")
+                    gather_last=gather, readout=readout, gated=name not in ("prefill-1layer", "cpu-1024"))
 
 
 def inputs(w: Workload, label: str, gen: torch.Generator | None = None) -> torch.Tensor:
@@ -184,7 +195,7 @@ def hbm_bytes(w: Workload, gated: tuple[str, ...] = ()) -> float:
     total = 0.0
     for layer in w.layers:
         for label, lin in layer.items():
-            total += lin.int4.nbytes() if lin.int4 is not None else 0
+            total += lin.int4.nbytes() if lin.int4 is not None else 2.0 * lin.k * lin.out
             total += 2.0 * w.tokens * (lin.k + (lin.out // 2 if label in gated else lin.out))
             for a in present:
                 r = w.adapter_ranks[a]

@@ -65,16 +65,6 @@ int main() {
   expect("plan narrow base", b, 3);
   expect("plan split", mlora_int4_plan(2048, 12288, 12288, 4096, 4096, 1025, 128, 0, &b, &s, &r), MLORA_OK);
   expect("plan split base", b, 2);
-  expect("plan row tiles", mlora_int4_plan(2048, 4096, 4096, 256, 256, 65, 192, MLORA_FORCE_BASE_ROWTILE, &b, &s, &r),
-         MLORA_OK);
-  expect("plan row tiles base", b, 4);
-  expect("plan row tiles column blocks", r, 1);
-  expect("plan row tiles of a pool pass",
-         mlora_int4_plan(2048, 12288, 12288, 4096, 4096, 1025, 128, MLORA_FORCE_BASE_ROWTILE, &b, &s, &r), MLORA_OK);
-  expect("plan row tiles of a pool pass: column blocks", r, 3);
-  expect("plan forced row tiles on a width of 32 (a partial tile)",
-         mlora_int4_plan(64, 64, 32, 9, 9, 10, 16, MLORA_FORCE_BASE_ROWTILE, &b, &s, &r), MLORA_OK);
-  expect("plan forced row tiles base", b, 4);
   expect("plan fused", mlora_int4_plan(1024, 3072, 3072, 8704, 64, 17, 16, 0, &b, &s, &r), MLORA_OK);
   expect("plan fused base", b, 1);
   expect("plan fused shrink", s, 1);

@@ -102,3 +102,24 @@ def token_ids(adp: torch.Tensor, pool_rows: int, row_len: int | None = None,
               cu: torch.Tensor | None = None) -> np.ndarray:
     return token_adapters(adp.cpu().numpy(), pool_rows, row_len=row_len,
                           cu_seqlens=None if cu is None else cu.cpu().numpy())
+
+
+def reference_f32_gpu(lin: Lin, w: torch.Tensor, x: torch.Tensor, tok_adp: np.ndarray) -> torch.Tensor:
+    """oracle.layer.reference_f32 evaluated on the GPU, for the rtol/atol check of every row of a pass too large for
+    the CPU: x W^T + (x A^T) sB^T from the same bfloat16 values in float32 (w: the oracle's dequantised (out, k)
+    weights; the adapters read back from the pool as the oracle reads them)."""
+    dev = x.device
+    xf = x.float()
+    y = xf @ w.to(dev).float().T.contiguous()
+    edges = np.concatenate([[0], np.cumsum(lin.sizes)]).astype(int)
+    for a, ups in oracle_adapters(lin, np.unique(tok_adp)).items():
+        idx = torch.from_numpy(np.nonzero(tok_adp == a)[0]).to(dev)
+        if idx.numel() == 0:
+            continue
+        xs = xf.index_select(0, idx)
+        for j, upd in enumerate(ups):
+            if upd is None:
+                continue
+            a_mat, sb = (t.to(dev).float() for t in upd)
+            y[idx, int(edges[j]):int(edges[j + 1])] += (xs @ a_mat.T.contiguous()) @ sb.T.contiguous()
+    return y

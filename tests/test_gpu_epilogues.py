@@ -93,10 +93,8 @@ def test_silu_mul(rows: int, inter: int) -> None:
 def test_silu_mul_over_every_bf16_gate() -> None:
     """All 65536 bf16 gate values (with up = 1, then random ups): bit for bit the oracle's rounding wherever exp(-g)
     is finite in float32; below g of about -88.7, where the reference's float32 formula overflows exp and gives
-    g / inf = -0, bit for bit that formula (the float64 oracle keeps a tiny nonzero value there). Two gate values
-    differ, both from the kernels' reciprocal correction step (q0 + fma(-q0, d, g) / d): g = -0 gives +0 (the formula
-    -0) and g = +inf gives NaN (the formula +inf); handling them in the kernels' rare IEEE-division branch cost the
-    gated prefill launch 1-2%, and neither value comes out of a finite product."""
+    g / inf = -0, bit for bit that formula (the float64 oracle keeps a tiny nonzero value there). Signed zeros and
+    infinities included: g = -0 gives -0 * u and g = +inf gives inf * u, as the formula does."""
     g = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(256, 256)
     gf = from_bits(g).float()
     with np.errstate(over="ignore", invalid="ignore"):
@@ -113,10 +111,10 @@ def test_silu_mul_over_every_bf16_gate() -> None:
         f32 = bits(((gf / (1.0 + torch.exp(-gf))).to(torch.bfloat16).float() * uf).to(torch.bfloat16))
         want = np.where(overflow, f32, want)
         nan_got, nan_want = np.isnan(from_bits(y).float().numpy()), np.isnan(from_bits(want).float().numpy())
-        special = (g == 0x8000) | (g == 0x7F80)  # -0 and +inf
-        assert np.array_equal(nan_got & ~special, nan_want & ~special)
-        differ = (y != want) & ~nan_got & ~special
+        assert np.array_equal(nan_got, nan_want)
+        differ = (y != want) & ~nan_got
         assert not differ.any(), f"{int(differ.sum())} gates differ, e.g. {[hex(v) for v in g[differ][:8]]}"
+        assert y[128, 0] == (0x8000 if u[128, 0] < 0x8000 else 0)  # g = -0 (row 128, column 0): -0 * u
 
 
 def test_epilogues_are_deterministic_and_replay_in_a_graph() -> None:
@@ -153,46 +151,57 @@ def test_epilogues_refuse_bad_arguments() -> None:
         silu_mul(torch.zeros(4, 32, device="cuda"))
 
 
-FUSED_CASES = {  # name: (tokens per request, requests, adapters, gate/up width, inputs, tiles, the kernel chosen)
-    "decode-rowtile": (1, 160, 12, 512, 2048, "rowtile", "rowtile"),
-    "decode-rowtile-wide": (1, 256, 64, 6144, 2048, "rowtile", "rowtile"),  # 192-column tiles, one per CU
-    "decode-narrow": (1, 160, 12, 512, 2048, None, "narrow"),
-    "decode-narrow-ranges": (1, 96, 12, 256, 1024, "narrow-4", "narrow"),
-    "decode-few-tokens": (1, 5, 12, 256, 512, "narrow", "narrow"),
-    "decode-few-tokens-rowtile": (1, 5, 12, 256, 512, "rowtile", "rowtile"),
-    "decode-split": (1, 600, 48, 256, 1024, None, "split"),
-    "decode-rowtile-many": (1, 600, 48, 256, 1024, "rowtile", "rowtile"),
-    "prefill-fused": (64, 24, 12, 384, 1024, None, "mfma"),
-    "prefill-tail": (40, 26, 12, 128, 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
+# name: (tokens per request, requests, adapters, gate/up width, inputs, tiles, the kernel chosen, rank capacity of gate
+# and of up). At capacity c the adapters' live ranks cycle through RANKS[c]: c itself among them, so the sB rows at
+# the capacity's own stride are read (64: finish_gated_columns<8>, the gated 256 x 256 kernel's second staged buffer,
+# the narrow kernel's ranks 33..64; 40 and 48: up's ranks across both staged buffers of the 256 x 256 kernel).
+RANKS = {32: (8, 16, 32), 40: (40, 8, 24), 48: (16, 48, 40), 64: (8, 16, 32, 64, 40, 56)}
+FUSED_CASES = {
+    "decode-narrow": (1, 160, 12, 512, 2048, None, "narrow", 32),
+    "decode-narrow-cap64": (1, 256, 64, 512, 2048, None, "narrow", 64),  # decode-28l's gate_up, narrower
+    "decode-narrow-cap48": (1, 200, 24, 256, 1024, None, "narrow", 48),
+    "decode-narrow-ranges": (1, 96, 12, 256, 1024, "narrow-4", "narrow", 32),
+    "decode-narrow-ranges-cap64": (1, 96, 12, 256, 1024, "narrow-4", "narrow", 64),
+    "decode-narrow-one-range-cap64": (1, 256, 64, 512, 2048, "narrow-1", "narrow", 64),  # as decode-28l's gate_up
+    "decode-few-tokens": (1, 5, 12, 256, 512, "narrow", "narrow", 32),
+    "decode-split": (1, 600, 48, 256, 1024, None, "split", 32),
+    "decode-split-cap64": (1, 600, 48, 256, 1024, None, "split", 64),  # decode-pool-28l's gate_up, narrower
+    "prefill-fused": (64, 24, 12, 384, 1024, None, "mfma", 32),  # 1536 tokens: 224-row tiles
+    "prefill-fused-cap64": (64, 24, 12, 384, 1024, None, "mfma", 64),
+    "prefill-fused-cap48": (64, 24, 12, 384, 1024, None, "mfma", 48),
+    "prefill-fused-cap40": (80, 20, 12, 256, 512, None, "mfma", 40),
+    "prefill-tail": (40, 26, 12, 128, 512, "mfma", "mfma", 32),  # 1040 tokens: the last 256-row tile holds 16
 }
 
 
 @pytest.mark.parametrize("name", list(FUSED_CASES))
 def test_silu_mul_in_the_product_tile_equals_silu_mul_of_the_product(name: str) -> None:
     """int4_product(..., epilogue="silu_mul") on a gate_up group (gate then up, one width) against silu_mul of the
-    plain product (the same tiles), bit for bit, for every kernel family that takes it (row tiles of 64 and 192
-    columns, narrow with and without input ranges, few tokens, split, the 256 x 256 tiles with a partial last tile), with the last-token rows gathered; and
-    against the oracle's silu_mul of the plain product."""
+    plain product (the same tiles), bit for bit, for every kernel family that takes it (narrow with and without input
+    ranges, few tokens, split, the 256 x 256 tiles of 224 and 256 rows with a partial last tile) at rank capacities
+    32, 40, 48 and 64, with the last-token rows gathered; against the oracle's silu_mul of the plain product; and the
+    plain product against the oracle's exact result and bound on every row."""
     from jeff_amd.fast_path import Workspace
     from jeff_amd.int4_kernels import int4_product
     from jeff_amd.int4_tiles import Int4Tiles
-    from tests.gpu_cases import make_case
+    from tests.gpu_cases import judge, make_case, token_ids
 
     from jeff_amd import _lib
     from jeff_amd.int4_tiles import int4_plan
 
-    row_len, requests, adapters, width, k, forced, kernel = FUSED_CASES[name]
+    row_len, requests, adapters, width, k, forced, kernel, cap = FUSED_CASES[name]
     print(f"fused silu_mul {name}", flush=True)
-    ranks = {a: [(8, 16, 32)[a % 3], (16, 8, 32)[a % 3]] for a in range(1, adapters + 1)}
-    case = make_case([width, width], k, 128, True, ranks, [32, 32], width + k)
+    cyc = RANKS[cap]
+    ranks = {a: [cyc[a % len(cyc)], cyc[(a + 1) % len(cyc)]] for a in range(1, adapters + 1)}
+    case = make_case([width, width], k, 128, True, ranks, [cap, cap], width + k)
     lin = case.lin
     tokens = row_len * requests
     rng = np.random.default_rng(tokens)
     adp = torch.tensor(rng.integers(0, adapters + 1, requests).astype(np.int32), device="cuda")
     x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
     ws = Workspace(tokens, row_len, max_rank=lin.rank)
-    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-4": Int4Tiles("narrow", "segment", 4),
-             "split": Int4Tiles("split", "segment"), "rowtile": Int4Tiles("rowtile", "segment"),
+    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-1": Int4Tiles("narrow", "segment", 1),
+             "narrow-4": Int4Tiles("narrow", "segment", 4), "split": Int4Tiles("split", "segment"),
              "mfma": Int4Tiles("mfma", "mfma")}[forced]
     flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_SILU_MUL
     assert int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)[0] == kernel
@@ -206,6 +215,8 @@ def test_silu_mul_in_the_product_tile_equals_silu_mul_of_the_product(name: str) 
     assert torch.equal(last, fused[row_len - 1::row_len])
     y_exact, y_bits, _ = oracle_silu_mul(bits(plain))
     check_close(fused, y_exact, y_bits, f"fused silu_mul {name}")
+    r = judge(lin, case.w, x, token_ids(adp, adapters + 1, row_len=row_len), plain)
+    assert r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, f"{name}: {r}"
 
 
 def test_silu_mul_epilogue_refusals() -> None:
@@ -222,17 +233,20 @@ def test_silu_mul_epilogue_refusals() -> None:
         int4_product(case.lin, x, Workspace(8, 1, max_rank=16), adp, epilogue="gelu")
 
 
-RESIDUAL_CASES = {  # name: (tokens per request, requests, adapters, matrix widths, inputs, tiles, the kernel chosen)
-    "decode-rowtile": (1, 160, 12, [512], 2048, "rowtile", "rowtile"),
-    "decode-rowtile-two": (1, 256, 64, [1024, 1024], 6144, "rowtile", "rowtile"),  # the down product's inputs
-    "decode-narrow": (1, 160, 12, [512], 2048, None, "narrow"),
-    "decode-narrow-ranges": (1, 96, 12, [256], 1024, "narrow-4", "narrow"),
-    "decode-few-tokens": (1, 5, 12, [256], 512, None, "narrow"),  # 5 tokens: the narrow product, not the GEMV
-    "decode-split": (1, 600, 48, [256], 1024, None, "split"),
-    "decode-rowtile-many": (1, 600, 48, [256], 1024, "rowtile", "rowtile"),
-    "prefill-fused": (64, 24, 12, [384, 128], 1024, None, "mfma"),
-    "prefill-small": (20, 6, 12, [256], 512, "mfma", "mfma"),  # 120 tokens: still the 256 x 256 kernel
-    "prefill-tail": (40, 26, 12, [128], 512, "mfma", "mfma"),  # 1040 tokens: the last 256-row tile holds 16
+RESIDUAL_CASES = {  # name: (tokens per request, requests, adapters, matrix widths, inputs, tiles, the kernel chosen,
+    # rank capacity of every matrix; the live ranks cycle through RANKS[capacity])
+    "decode-narrow": (1, 160, 12, [512], 2048, None, "narrow", 32),
+    "decode-narrow-ranges": (1, 96, 12, [256], 1024, "narrow-4", "narrow", 32),
+    "decode-o-cap64": (1, 256, 64, [2048], 2048, None, "narrow", 64),  # decode-28l's o product
+    "decode-down-cap64": (1, 256, 64, [2048], 6144, None, "narrow", 64),  # decode-28l's down product
+    "decode-one-range-cap64": (1, 256, 64, [1024], 2048, "narrow-1", "narrow", 64),
+    "decode-few-tokens": (1, 5, 12, [256], 512, None, "narrow", 32),  # 5 tokens: the narrow product, not the GEMV
+    "decode-split": (1, 600, 48, [256], 1024, None, "split", 32),
+    "decode-split-cap64": (1, 600, 48, [256, 128], 1024, None, "split", 64),  # finish_columns<8>
+    "prefill-fused": (64, 24, 12, [384, 128], 1024, None, "mfma", 32),
+    "prefill-fused-cap64": (64, 24, 12, [384, 128], 1024, None, "mfma", 64),
+    "prefill-small": (20, 6, 12, [256], 512, "mfma", "mfma", 32),  # 120 tokens: still the 256 x 256 kernel
+    "prefill-tail": (40, 26, 12, [128], 512, "mfma", "mfma", 32),  # 1040 tokens: the last 256-row tile holds 16
 }
 
 
@@ -245,20 +259,21 @@ def test_residual_add_in_the_product_tile_equals_add_rms_of_the_product(name: st
     from jeff_amd.fast_path import Workspace
     from jeff_amd.int4_kernels import int4_product
     from jeff_amd.int4_tiles import Int4Tiles, int4_plan
-    from tests.gpu_cases import make_case
+    from tests.gpu_cases import judge, make_case, token_ids
 
-    row_len, requests, adapters, widths, k, forced, kernel = RESIDUAL_CASES[name]
+    row_len, requests, adapters, widths, k, forced, kernel, cap = RESIDUAL_CASES[name]
     print(f"fused residual add {name}", flush=True)
-    ranks = {a: [(8, 16, 32)[(a + j) % 3] for j in range(len(widths))] for a in range(1, adapters + 1)}
-    case = make_case(widths, k, 128, True, ranks, [32] * len(widths), sum(widths) + k + 7)
+    cyc = RANKS[cap]
+    ranks = {a: [cyc[(a + j) % len(cyc)] for j in range(len(widths))] for a in range(1, adapters + 1)}
+    case = make_case(widths, k, 128, True, ranks, [cap] * len(widths), sum(widths) + k + 7)
     lin = case.lin
     tokens = row_len * requests
     rng = np.random.default_rng(tokens + 1)
     adp = torch.tensor(rng.integers(0, adapters + 1, requests).astype(np.int32), device="cuda")
     x = torch.randn(tokens, k, device="cuda").to(torch.bfloat16)
     ws = Workspace(tokens, row_len, max_rank=lin.rank)
-    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-4": Int4Tiles("narrow", "segment", 4),
-             "split": Int4Tiles("split", "segment"), "rowtile": Int4Tiles("rowtile", "segment"),
+    tiles = {None: None, "narrow": Int4Tiles("narrow", "segment"), "narrow-1": Int4Tiles("narrow", "segment", 1),
+             "narrow-4": Int4Tiles("narrow", "segment", 4), "split": Int4Tiles("split", "segment"),
              "mfma": Int4Tiles("mfma", "mfma")}[forced]
     flags = (0 if tiles is None else tiles.flags()) | _lib.EPILOGUE_RESIDUAL
     plan = int4_plan(lin.int4.columns, k, tokens, requests, adapters + 1, lin.rank, lin.out, flags)
@@ -276,6 +291,8 @@ def test_residual_add_in_the_product_tile_equals_add_rms_of_the_product(name: st
     assert torch.equal(last, res[row_len - 1::row_len])
     xo_bits, _, _ = oracle_add_rms(bits(r0), bits(plain), np.ones(lin.out, np.float32))
     assert np.array_equal(bits(res), xo_bits)
+    r = judge(lin, case.w, x, token_ids(adp, adapters + 1, row_len=row_len), plain)
+    assert r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, f"{name}: {r}"
 
 
 def test_residual_epilogue_refusals() -> None:

@@ -176,3 +176,49 @@ def test_switching_adapter_touches_the_pool_with_no_pytorch_operation() -> None:
             torch.cuda.synchronize()
             assert torch.equal(out, eager)
     assert switching.seen == [], switching.seen
+
+
+def test_two_graphs_on_one_workspace_at_growing_sizes() -> None:
+    """A workspace named no shapes, so its float32 partials grow with the products: a graph records a narrow product
+    over eight input ranges on the first buffer, an eager product of a wider group then needs a larger one, a tensor
+    is allocated after that growth, and a second graph records the wider product. The first graph keeps its buffer
+    (the workspace never frees one a graph may hold), so replays of both graphs, new adapter ids each time, match the
+    oracle on every row, and the tensor allocated after the growth is never written."""
+    ranks = {a: [(8, 16)[a % 2]] for a in range(1, 7)}
+    small = make_case([256], 1024, 128, True, ranks, [16], 91)
+    wide = make_case([1024], 1024, 128, True, ranks, [16], 92)
+    requests = 256
+    tiles = Int4Tiles("narrow", "segment", 8)
+    rng = np.random.default_rng(5)
+    adp = torch.tensor(rng.integers(0, 7, requests).astype(np.int32), device="cuda")
+    x = torch.randn(requests, 1024, device="cuda").to(DT)
+    ws = Workspace(requests, 1, max_rank=16, max_requests=requests)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        int4_product(small.lin, x, ws, adp, tiles=tiles)
+    stream.synchronize()
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=stream):
+        y1 = int4_product(small.lin, x, ws, adp, tiles=tiles)
+    first = ws._part
+    with torch.cuda.stream(stream):
+        int4_product(wide.lin, x, ws, adp, tiles=tiles)  # grows the partials
+    stream.synchronize()
+    assert ws._part is not first and any(t is first for t in ws._retired)
+    sentinel = torch.full((4 << 20,), 7.0, device="cuda")
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=stream):
+        y2 = int4_product(wide.lin, x, ws, adp, tiles=tiles)
+    pool_rows = small.lin.pool.shape[0]
+    for rep in range(3):
+        adp.copy_(torch.tensor(rng.integers(0, 7, requests).astype(np.int32), device="cuda"))
+        x.copy_(torch.randn(requests, 1024, device="cuda").to(DT))
+        g1.replay()
+        g2.replay()
+        torch.cuda.synchronize()
+        tok = token_ids(adp, pool_rows, row_len=1)
+        for case, y in ((small, y1), (wide, y2)):
+            r = judge(case.lin, case.w, x, tok, y)
+            assert r["beyond_bound"] == 0 and r["outside_tolerance"] == 0, f"replay {rep}: {r}"
+        assert bool((sentinel == 7.0).all()), f"replay {rep} wrote into memory allocated after the growth"

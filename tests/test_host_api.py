@@ -130,12 +130,6 @@ def test_kernel_choice_rule() -> None:
     assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("narrow", "segment")
     assert int4_tiles(4096, 2048, 257, 257, 65) == Int4Tiles("split", "segment")
     assert int4_tiles(12288, 2048, 4096, 4096, 1025) == Int4Tiles("split", "segment")
-    from jeff_amd import _lib
-    from jeff_amd.int4_tiles import int4_plan
-    # the row-tile product when forced: column blocks per wave chosen to give every CU a workgroup (12288 columns
-    # cut into 192-column tiles, 4096 into 64-column ones)
-    assert int4_plan(4096, 2048, 256, 256, 65, flags=_lib.FORCE_BASE_ROWTILE) == ("rowtile", "segment", 1)
-    assert int4_plan(12288, 2048, 256, 256, 65, flags=_lib.FORCE_BASE_ROWTILE) == ("rowtile", "segment", 3)
     assert int4_tiles(3072, 1024, 8704, 64, 17) == Int4Tiles("mfma", "mfma")
     with pytest.raises(ValueError):
         int4_tiles(100, 1024, 4)
@@ -215,3 +209,26 @@ def test_a_route_is_shared_only_inside_the_capture_that_launched_it() -> None:
     rec = record(11)
     del adp                                                  # the recorded tensor is gone
     assert not reusable(rec, torch.zeros(4, dtype=torch.int32), 4, 5, 7, 11)
+
+
+def test_partials_bound_covers_every_automatic_product() -> None:
+    """mlora_int4_partials_bound (a workspace's up-front size for its shapes) is at least the float32 partials of the
+    kernels the library picks for every token count up to the bound's own, on the decoder's groups (host only)."""
+    from jeff_amd import _lib
+    from jeff_amd.int4_tiles import int4_plan
+
+    h = _lib.lib()
+    for k, out in ((2048, 4096), (2048, 2048), (2048, 12288), (6144, 2048), (1024, 3072), (512, 320)):
+        cols = -(-out // 64) * 64
+        for tokens in (1, 9, 200, 256, 257, 1000, 4096, 20000):
+            bound = h.mlora_int4_partials_bound(k, cols, out, tokens)
+            for t in sorted({1, 2, 9, 255, 256, 257, 511, 512, 513, 1024, tokens // 2 + 1, tokens}):
+                if t > tokens:
+                    continue
+                for requests in (min(t, 8192), max(1, t // 40)):
+                    base, _, ranges = int4_plan(cols, k, t, requests, 1025, 64, out)
+                    need = {"narrow": ranges * (cols // 64) * 256 * 64 * 4 if ranges > 1 else 0,
+                            "split": (ranges * t * cols * 4 + 255) // 256 * 256}.get(base, 0)
+                    assert bound >= need, (k, out, tokens, t, requests, base, ranges, need, bound)
+    assert h.mlora_int4_partials_bound(100, 64, 64, 8) == 0
+    assert h.mlora_int4_partials_bound(2048, 4096, 4096, 0) == 0
