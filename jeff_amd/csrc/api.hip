@@ -85,6 +85,7 @@ bool shrink_on_mfma(const mlora_route_t* r, int32_t pool_rows, int32_t flags) {
 enum class Base { gemv, fused, split, narrow };
 
 constexpr int64_t kNarrowMaxTokens = 256;  // the narrow kernel's row tile holds every token of the pass
+constexpr int64_t kSplitMaxTokens = 1024;  // short-segment passes of this many tokens or more take the fused tiles
 
 // The split product runs the 256 x 256 kernel (32-bit x offsets) and stages first factors of at most
 // MLORA_SPLIT_MAX_RANK stacked ranks.
@@ -134,8 +135,13 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
     *out = Base::gemv;
   } else if (long_segments(r, L->pool_rows) || !split_fits(w, L, r, x_stride)) {
     *out = Base::fused;
+  } else if (r->tokens <= kNarrowMaxTokens) {
+    *out = Base::narrow;
   } else {
-    *out = r->tokens <= kNarrowMaxTokens ? Base::narrow : Base::split;
+    // short segments, more tokens: from kSplitMaxTokens on, the 256 x 256 tiles with the LoRA term fused (each
+    // segment's bookkeeping from lane tables) beat the split product, whose float32 partials make a round trip
+    // through memory
+    *out = r->tokens < kSplitMaxTokens ? Base::split : Base::fused;
   }
   if (fs != 0 && *out != Base::narrow) return MLORA_EUNSUPPORTED;
   if (gated) {

@@ -224,6 +224,225 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     }
   }
   auto half_of = [](uint64_t pair, int i) __attribute__((always_inline)) { return (int)(uint32_t)(pair >> (32 * i)); };
+  // LoRA second factor. The tile's rows of the first factor (sorted order, 64 ranks of a matrix at a time) are staged
+  // in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come straight from
+  // memory as MFMA operands ahead of their products (three segments in the plain form, one in the gated form, whose
+  // wave-dependent matrix leaves fewer registers), and the products are added with the first
+  // factors of rows outside the segment, and ranks past the adapter's live rank, set to zero. A decode-shaped tile
+  // crosses ~64 segments, so their bookkeeping is read into lane tables (lane i: segment c0 + i's adapter, live rank
+  // and bounds, 64 segments at a time) and taken with readlane, with no memory latency per segment; the first two
+  // segments' adapters and live ranks of the first matrix were read in the prologue, so a prefill tile (one or two
+  // segments) starts its sB loads at once. st0 (and st1, the gated form's second buffer) are the LDS buffers the first
+  // factors are staged in (two of the x ring, idle after the K loop).
+  auto lora_term = [&](uint16_t* st0, uint16_t* st1) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
+    // one pass over the segments: `stage` stages the first factors, then per chunk of 64 segments the lane tables
+    // (ta, tb, te: adapter and bounds; tl: live rank of matrix j) and the segments' products, sB three ahead.
+    // `ahead`: the prologue's read-ahead applies (the first chunk of matrix jlo); `rc` the rank chunk
+    auto pass = [&](int j, int rc, bool ahead, auto&& stage, auto&& load_seg, auto&& apply_seg)
+        __attribute__((always_inline)) {
+      stage();
+      __builtin_amdgcn_sched_barrier(0);  // the staging loads are issued before every load below
+      for (int c0 = s_lo; c0 <= s_hi; c0 += kWave) {
+        const int cend = min(c0 + kWave - 1, s_hi);  // the chunk's last segment
+        const int sc = min(c0 + lane, cend);
+        const int ta = r.seg_adapter[sc], tb = r.seg_start[sc], te = r.seg_start[sc + 1];
+        const int tl = ta == 0 ? 0 : live_rank(L, ta, j);
+        const bool pre = ahead && c0 == s_lo;
+        // segment s's adapter and live rank (s clamped to the chunk: past it the loads re-read its last segment and
+        // rk is 0)
+        auto seg = [&](int s, int& a, int& live) __attribute__((always_inline)) {
+          const int i = min(s, cend) - c0;
+          if (pre && i < 2) {
+            a = half_of(a_pre, i);
+            live = half_of(GATED && j == 1 ? live_up : live_pre, i);
+          } else {
+            a = __builtin_amdgcn_readlane(ta, i);
+            live = __builtin_amdgcn_readlane(tl, i);
+          }
+        };
+        uint4 q0[4], q1[4], q2[4];
+        int k0, k1, k2;
+        auto load = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+          int a, live;
+          seg(s, a, live);
+          load_seg(a, live, bv);
+          rk = s <= cend ? min(live - rc, kRankChunk) : 0;
+        };
+        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+          if (rk <= 0) return;
+          const int i = s - c0;
+          // the bounds relative to the tile (tile rows and segment bounds are below 2^31)
+          apply_seg(__builtin_amdgcn_readlane(tb, i) - (int)p0, __builtin_amdgcn_readlane(te, i) - (int)p0, bv, rk);
+        };
+        load(c0, q0, k0);
+        load(c0 + 1, q1, k1);
+        load(c0 + 2, q2, k2);
+        if (c0 == s_lo) {
+          MLORA_WAIT_VM(12);  // the staged first factors have landed (the sB loads may be in flight)
+          lds_sync();
+        }
+        for (int s = c0; s <= cend; s += 3) {
+          apply(s, q0, k0);
+          load(s + 3, q0, k0);
+          apply(s + 1, q1, k1);
+          load(s + 4, q1, k1);
+          apply(s + 2, q2, k2);
+          load(s + 5, q2, k2);
+        }
+      }
+    };
+    if constexpr (GATED) {
+      // Gated: gate and up have one capacity c <= 64 (the host checks it), so both matrices' first factors are
+      // staged at once and each wave adds only its own matrix's term (waves 0..3 gate, waves 4..7 up). When 2c <= 64
+      // the stacked ranks [0, 2c) fit the first buffer (up's from chunk c / 8); otherwise the first buffer holds
+      // stacked ranks [0, 64) (gate's c ranks first) and the second stacked ranks [c, c + 64) (up's, from chunk 0).
+      // Ranks past a matrix's own c are the other matrix's or the next row's; they are masked by the live rank. The
+      // segments' bookkeeping is read per segment (scalar loads, one segment ahead): the lane tables of the plain
+      // form, with a wave-dependent matrix, left the compiler short of registers.
+      const bool two = L.rank_cap > kRankChunk;
+      const int j = wave < 4 ? 0 : 1, capj = L.cap[j];
+      lds_sync();  // every wave is done reading the x ring
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 1 && !two) break;
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+          const int row = (8 * i + wave) * 8 + (lane >> 3);
+          const uint32_t off =
+              (uint32_t)(((p0 + row) * L.rank_cap + h * L.cap[0] + (swz_slot(row, lane & 7) << 3)) * 2);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)((h ? st1 : st0) + (8 * i + wave) * 8 * kTK),
+                                                   16, off, 0, 0, 0);
+        }
+      }
+      // the lane's staged rows: row mb * 32 + (lane & 31) of the buffer holding its matrix's ranks, whose 16-byte
+      // chunk c sits in slot c ^ key; the matrix's ranks start at chunk o8 (16 k16 + 8 (lane >> 5) then in chunk
+      // o8 + 2 k16 + (lane >> 5) <= 7 for every k16 below the capacity)
+      const uint4* mrow = reinterpret_cast<const uint4*>(j == 1 && two ? st1 : st0) + (lane & 31) * 8;
+      const int key = ((lane & 31) >> 1) & 7;
+      const int cb = (j == 1 && !two ? capj / 8 : 0) + (lane >> 5);
+      const int ccol = wcol - (j ? inter : 0);        // the lane's column inside its matrix
+      __builtin_amdgcn_sched_barrier(0);  // the staging loads are issued before every load below
+      // per chunk of 64 segments, lane tables (lane i: segment c0 + i's adapter, bounds relative to the tile, and
+      // live rank of the wave's matrix), then each segment's sB operands one segment ahead of its products
+      for (int c0 = s_lo; c0 <= s_hi; c0 += kWave) {
+        const int cend = min(c0 + kWave - 1, s_hi);  // the chunk's last segment
+        const int sc = min(c0 + lane, cend);
+        const int ta = r.seg_adapter[sc];
+        const int tb = r.seg_start[sc] - (int)p0, te = r.seg_start[sc + 1] - (int)p0;  // tile rows: below 2^31
+        const int tl = ta == 0 ? 0 : live_rank(L, ta, j);
+        // sB operands of segment s for ranks 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk` (0 past the
+        // chunk: the loads then re-read its last segment's)
+        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+          const int i = min(s, cend) - c0;
+          int a, live;
+          if (c0 == s_lo && i < 2) {  // read ahead in the prologue
+            a = half_of(a_pre, i);
+            live = half_of(j == 0 ? live_pre : live_up, i);
+          } else {
+            a = __builtin_amdgcn_readlane(ta, i);
+            live = __builtin_amdgcn_readlane(tl, i);
+          }
+          rk = s <= cend ? live : 0;
+          const int sbs = sb_stride(live, capj);
+          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            const int q = min(16 * k16 + 8 * (lane >> 5), sbs - 8);
+            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+          }
+        };
+        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+          if (rk <= 0) return;
+          const int sb = __builtin_amdgcn_readlane(tb, s - c0), se = __builtin_amdgcn_readlane(te, s - c0);
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
+            const int row = mb * 32 + (lane & 31);
+            const bool rin = row >= sb && row < se;
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) {
+              if (16 * k16 >= rk) break;
+              uint4 av = mrow[mb * 256 + ((cb + 2 * k16) ^ key)];
+              av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+              acc[mb] = mfma32(bv[k16], av, acc[mb]);
+            }
+          }
+        };
+        uint4 b0[4], b1[4];
+        int rk0, rk1;
+        load_b(c0, b0, rk0);
+        if (c0 == s_lo) {
+          MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
+          lds_sync();
+        }
+        for (int s = c0; s <= cend; s += 2) {
+          load_b(s + 1, b1, rk1);
+          apply(s, b0, rk0);
+          if (s + 1 > cend) break;
+          load_b(s + 2, b0, rk0);
+          apply(s + 1, b1, rk1);
+        }
+      }
+    } else {
+      const int jhi = matrix_of(L, min(n0 + kTN, n_out) - 1);
+      for (int j = jlo; j <= jhi; ++j) {
+        const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
+        // the wave's column inside matrix j (others get zero operands)
+        const int cc = wc0 + (lane & 31);
+        const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
+        const int ccol = (cin ? cc : oj) - oj;
+        for (int rc = 0; rc < capj; rc += kRankChunk) {
+          pass(j, rc, j == jlo,
+               // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
+               [&]() __attribute__((always_inline)) {
+                 lds_sync();  // every wave is done with the previous chunk's rows
+#pragma unroll
+                 for (int i = 0; i < kXLoads; ++i) {
+                   const int row = (8 * i + wave) * 8 + (lane >> 3);
+                   const uint32_t off =
+                       (uint32_t)(((p0 + row) * L.rank_cap + rho + rc + (swz_slot(row, lane & 7) << 3)) * 2);
+                   __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)(st0 + (8 * i + wave) * 8 * kTK), 16,
+                                                            off, 0, 0, 0);
+                 }
+               },
+               // sB operands for ranks rc + 16 k16 + 8 (lane >> 5) .. +7 (clamped to the adapter's block)
+               [&](int a, int live, uint4 (&bv)[4]) __attribute__((always_inline)) {
+                 const int sbs = sb_stride(live, capj);  // the adapter's sB row stride (at least 8: capj > rc >= 0)
+                 const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+#pragma unroll
+                 for (int k16 = 0; k16 < 4; ++k16) {
+                   const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
+                   bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+                 }
+               },
+               [&](int sb, int se, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+                 // (sb, se: the segment's bounds relative to the tile's first row)
+#pragma unroll
+                 for (int k16 = 0; k16 < 4; ++k16)
+                   bv[k16] = cin ? keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                 for (int mb = 0; mb < MB; ++mb) {
+                   if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
+                   const int row = mb * 32 + (lane & 31);
+                   const bool rin = row >= sb && row < se;
+#pragma unroll
+                   for (int k16 = 0; k16 < 4; ++k16) {
+                     if (16 * k16 >= rk) break;
+                     uint4 av =
+                         reinterpret_cast<const uint4*>(st0)[swz(mb * 32 + (lane & 31), 2 * k16 + (lane >> 5)) >> 3];
+                     av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+                     acc[mb] = mfma32(bv[k16], av, acc[mb]);
+                   }
+                 }
+               });
+        }
+      }
+    }
+  };
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
   load_a(g_x0, 0, a);
@@ -276,172 +495,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     return;
   }
 
-  // LoRA second factor. The tile's rows of the first factor (sorted order, ranks rc .. rc + 63 of matrix j) are
-  // staged in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come
-  // straight from memory as MFMA operands (the next segment's issued before the current one's products), and the
-  // products are added with the first factors of rows outside the segment, and ranks past the adapter's live rank,
-  // set to zero. The first two segments' adapters and live ranks of the first matrix were read in the prologue.
-  if constexpr (GATED) {
-    // Gated: gate and up have one capacity c <= 64 (the host checks it), so both matrices' first factors are staged
-    // at once and each wave adds only its own matrix's term (waves 0..3 gate, waves 4..7 up). When 2c <= 64 the
-    // stacked ranks [0, 2c) fit the first buffer (up's from chunk c / 8); otherwise the first buffer holds stacked
-    // ranks [0, 64) (gate's c ranks first) and the second stacked ranks [c, c + 64) (up's, from chunk 0). Ranks past a
-    // matrix's own c are the other matrix's or the next row's; they are masked by the live rank.
-    if (lora) {
-      const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
-      const bool two = L.rank_cap > kRankChunk;
-      const int j = wave < 4 ? 0 : 1, capj = L.cap[j];
-      lds_sync();  // every wave is done reading the x ring
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (h == 1 && !two) break;
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-          const int row = (8 * i + wave) * 8 + (lane >> 3);
-          const uint32_t off =
-              (uint32_t)(((p0 + row) * L.rank_cap + h * L.cap[0] + (swz_slot(row, lane & 7) << 3)) * 2);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)((h ? g_x1 : g_x0) + (8 * i + wave) * 8 * kTK),
-                                                   16, off, 0, 0, 0);
-        }
-      }
-      // the lane's staged rows: row mb * 32 + (lane & 31) of the buffer holding its matrix's ranks, whose 16-byte
-      // chunk c sits in slot c ^ key; the matrix's ranks start at chunk o8 (16 k16 + 8 (lane >> 5) then in chunk
-      // o8 + 2 k16 + (lane >> 5) <= 7 for every k16 below the capacity)
-      const uint4* mrow = reinterpret_cast<const uint4*>(j == 1 && two ? g_x1 : g_x0) + (lane & 31) * 8;
-      const int key = ((lane & 31) >> 1) & 7;
-      const int cb = (j == 1 && !two ? capj / 8 : 0) + (lane >> 5);
-      const int ccol = wcol - (j ? inter : 0);        // the lane's column inside its matrix
-      // sB operands of segment s for ranks 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
-      auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
-        int a, live;
-        if (s - s_lo < 2) {  // read ahead in the prologue
-          a = half_of(a_pre, s - s_lo);
-          live = half_of(j == 0 ? live_pre : live_up, s - s_lo);
-        } else {
-          a = r.seg_adapter[s];
-          live = a == 0 ? 0 : live_rank(L, a, j);
-        }
-        rk = live;
-        const int sbs = sb_stride(live, capj);
-        const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
-#pragma unroll
-        for (int k16 = 0; k16 < 4; ++k16) {
-          const int q = min(16 * k16 + 8 * (lane >> 5), sbs - 8);
-          bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
-        }
-      };
-      auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
-        if (rk <= 0) return;
-        const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
-#pragma unroll
-        for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const int64_t r0 = p0 + mb * 32;
-          if (r0 >= se || r0 + 32 <= sb) continue;
-          const int64_t row = r0 + (lane & 31);
-          const bool rin = row >= sb && row < se;
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            if (16 * k16 >= rk) break;
-            uint4 av = mrow[mb * 256 + ((cb + 2 * k16) ^ key)];
-            av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-            acc[mb] = mfma32(bv[k16], av, acc[mb]);
-          }
-        }
-      };
-      uint4 b0[4], b1[4];
-      int rk0, rk1;
-      load_b(s_lo, b0, rk0);
-      MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
-      lds_sync();
-      for (int s = s_lo; s <= s_hi; s += 2) {
-        load_b(min(s + 1, s_hi), b1, rk1);
-        apply(s, b0, rk0);
-        if (s + 1 > s_hi) break;
-        load_b(min(s + 2, s_hi), b0, rk0);
-        apply(s + 1, b1, rk1);
-      }
-    }
-  }
-  if (lora && !GATED) {
-    const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
-    const int jhi = matrix_of(L, GATED ? inter + nt * 128 + 127 : min(n0 + kTN, n_out) - 1);
-    for (int j = jlo; j <= jhi; ++j) {
-      const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j], rho = rank_offset(L, j);
-      // the wave's column inside matrix j (others get zero operands)
-      const int cc = wc0 + (lane & 31);
-      const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
-      const int ccol = (cin ? cc : oj) - oj;
-      for (int rc = 0; rc < capj; rc += kRankChunk) {
-        // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
-        lds_sync();  // every wave is done with the previous chunk's rows
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-          const int row = (8 * i + wave) * 8 + (lane >> 3);
-          const uint32_t off =
-              (uint32_t)(((p0 + row) * L.rank_cap + rho + rc + (swz_slot(row, lane & 7) << 3)) * 2);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)(g_x0 + (8 * i + wave) * 8 * kTK), 16, off, 0, 0,
-                                                   0);
-        }
-        // sB operands of segment s for ranks rc + 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk`
-        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
-          int a, live;
-          if (j == jlo && s - s_lo < 2) {  // read ahead
-            a = half_of(a_pre, s - s_lo);
-            live = half_of(live_pre, s - s_lo);
-          } else {
-            a = r.seg_adapter[s];
-            live = a == 0 ? 0 : live_rank(L, a, j);
-          }
-          rk = min(live - rc, kRankChunk);
-          const int sbs = sb_stride(live, capj);  // the adapter's sB row stride (at least 8: capj > rc >= 0)
-          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            const int kk = 16 * k16 + 8 * (lane >> 5);
-            const int q = min(rc + kk, sbs - 8);
-            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
-          }
-        };
-        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
-          if (rk <= 0) return;
-          const int64_t sb = r.seg_start[s], se = r.seg_start[s + 1];
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16)
-            bv[k16] = cin ? keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            const int64_t r0 = p0 + mb * 32;
-            if (r0 >= se || r0 + 32 <= sb) continue;
-            const int64_t row = r0 + (lane & 31);
-            const bool rin = row >= sb && row < se;
-#pragma unroll
-            for (int k16 = 0; k16 < 4; ++k16) {
-              if (16 * k16 >= rk) break;
-              uint4 av = reinterpret_cast<const uint4*>(g_x0)[swz(mb * 32 + (lane & 31), 2 * k16 + (lane >> 5)) >> 3];
-              av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-              acc[mb] = mfma32(bv[k16], av, acc[mb]);
-            }
-          }
-        };
-        uint4 b0[4], b1[4];
-        int rk0, rk1;
-        load_b(s_lo, b0, rk0);
-        MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
-        lds_sync();
-        for (int s = s_lo; s <= s_hi; s += 2) {
-          load_b(min(s + 1, s_hi), b1, rk1);
-          apply(s, b0, rk0);
-          if (s + 1 > s_hi) break;
-          load_b(min(s + 2, s_hi), b0, rk0);
-          apply(s + 1, b1, rk1);
-        }
-      }
-    }
-  }
+  if (lora) lora_term(g_x0, g_x1);
 
   // Single rounding to bf16 and the stores, through LDS (the whole tile at once): lane l holds, for row
   // mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave

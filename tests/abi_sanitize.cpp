@@ -63,8 +63,11 @@ int main() {
   expect("plan gemv base", b, 0);
   expect("plan narrow", mlora_int4_plan(2048, 4096, 4096, 256, 256, 65, 192, 0, &b, &s, &r), MLORA_OK);
   expect("plan narrow base", b, 3);
-  expect("plan split", mlora_int4_plan(2048, 12288, 12288, 4096, 4096, 1025, 128, 0, &b, &s, &r), MLORA_OK);
+  expect("plan split", mlora_int4_plan(2048, 12288, 12288, 600, 600, 1025, 128, 0, &b, &s, &r), MLORA_OK);
   expect("plan split base", b, 2);
+  expect("plan decode pool", mlora_int4_plan(2048, 12288, 12288, 4096, 4096, 1025, 128, 0, &b, &s, &r), MLORA_OK);
+  expect("plan decode pool base", b, 1);
+  expect("plan decode pool shrink", s, 0);
   expect("plan fused", mlora_int4_plan(1024, 3072, 3072, 8704, 64, 17, 16, 0, &b, &s, &r), MLORA_OK);
   expect("plan fused base", b, 1);
   expect("plan fused shrink", s, 1);

@@ -165,7 +165,9 @@ FUSED_CASES = {
     "decode-narrow-one-range-cap64": (1, 256, 64, 512, 2048, "narrow-1", "narrow", 64),  # as decode-28l's gate_up
     "decode-few-tokens": (1, 5, 12, 256, 512, "narrow", "narrow", 32),
     "decode-split": (1, 600, 48, 256, 1024, None, "split", 32),
-    "decode-split-cap64": (1, 600, 48, 256, 1024, None, "split", 64),  # decode-pool-28l's gate_up, narrower
+    "decode-split-cap64": (1, 600, 48, 256, 1024, None, "split", 64),
+    # 1536 one-token rows over 300 adapters: the 256 x 256 tiles with ~50 segments each (lane tables, 64 at a time)
+    "decode-tiles-cap64": (1, 1536, 300, 256, 1024, None, "mfma", 64),  # decode-pool-28l's gate_up, narrower
     "prefill-fused": (64, 24, 12, 384, 1024, None, "mfma", 32),  # 1536 tokens: 224-row tiles
     "prefill-fused-cap64": (64, 24, 12, 384, 1024, None, "mfma", 64),
     "prefill-fused-cap48": (64, 24, 12, 384, 1024, None, "mfma", 48),
@@ -243,6 +245,9 @@ RESIDUAL_CASES = {  # name: (tokens per request, requests, adapters, matrix widt
     "decode-few-tokens": (1, 5, 12, [256], 512, None, "narrow", 32),  # 5 tokens: the narrow product, not the GEMV
     "decode-split": (1, 600, 48, [256], 1024, None, "split", 32),
     "decode-split-cap64": (1, 600, 48, [256, 128], 1024, None, "split", 64),  # finish_columns<8>
+    # the 256 x 256 tiles on a decode-shaped pass (each tile's segments from lane tables, 64 at a time)
+    "decode-tiles-cap64": (1, 1536, 300, [384, 128], 1024, None, "mfma", 64),
+    "decode-tiles-many-segments": (1, 2048, 900, [256], 512, None, "mfma", 32),  # > 64 segments in a tile
     "prefill-fused": (64, 24, 12, [384, 128], 1024, None, "mfma", 32),
     "prefill-fused-cap64": (64, 24, 12, [384, 128], 1024, None, "mfma", 64),
     "prefill-small": (20, 6, 12, [256], 512, "mfma", "mfma", 32),  # 120 tokens: still the 256 x 256 kernel

@@ -129,7 +129,9 @@ def test_kernel_choice_rule() -> None:
     assert int4_tiles(4096, 2048, 8) == Int4Tiles("gemv", "segment")
     assert int4_tiles(4096, 2048, 256, 256, 65) == Int4Tiles("narrow", "segment")
     assert int4_tiles(4096, 2048, 257, 257, 65) == Int4Tiles("split", "segment")
-    assert int4_tiles(12288, 2048, 4096, 4096, 1025) == Int4Tiles("split", "segment")
+    assert int4_tiles(12288, 2048, 1023, 1023, 1025) == Int4Tiles("split", "segment")
+    # from 1024 tokens on, short segments take the 256 x 256 tiles with the LoRA term fused (segment-form first factor)
+    assert int4_tiles(12288, 2048, 4096, 4096, 1025) == Int4Tiles("mfma", "segment")
     assert int4_tiles(3072, 1024, 8704, 64, 17) == Int4Tiles("mfma", "mfma")
     with pytest.raises(ValueError):
         int4_tiles(100, 1024, 4)
@@ -145,7 +147,8 @@ def test_kernel_choice_with_epilogues() -> None:
     assert int4_plan(2048, 2048, 5, flags=_lib.EPILOGUE_RESIDUAL)[0] == "narrow"
     assert int4_plan(12288, 2048, 5, flags=_lib.EPILOGUE_SILU_MUL)[0] == "narrow"
     assert int4_plan(2048, 6144, 159488, 512, 129, 32, flags=_lib.EPILOGUE_RESIDUAL)[0] == "mfma"
-    assert int4_plan(2048, 6144, 4096, 4096, 1025, 64, flags=_lib.EPILOGUE_RESIDUAL)[0] == "split"
+    assert int4_plan(2048, 6144, 1000, 1000, 1025, 64, flags=_lib.EPILOGUE_RESIDUAL)[0] == "split"
+    assert int4_plan(2048, 6144, 4096, 4096, 1025, 64, flags=_lib.EPILOGUE_RESIDUAL)[0] == "mfma"
     with pytest.raises(ValueError, match="does not run"):
         int4_plan(2048, 2048, 5, flags=_lib.EPILOGUE_RESIDUAL | _lib.FORCE_BASE_GEMV)
     with pytest.raises(ValueError, match="invalid|argument"):
