@@ -44,7 +44,8 @@ __shared__ __attribute__((aligned(16))) uint16_t g_x3[kTM * kTK];  // the output
 __shared__ int32_t g_orig[kTM];  // the tile's rows: original token index, -1 past the tokens
 __shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it is, else -1
 
-// MB: 32-row blocks of a tile (8: 256 rows; 7: 224 rows, chosen by the host when it takes fewer rounds of tiles);
+// MB: 32-row blocks of a tile (8: 256 rows; 7: 224 and 4: 128 rows, chosen by the host when they take fewer rounds
+// of tiles);
 // GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none of it
 template <int MB, bool GATED>
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
@@ -582,9 +583,12 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 
 }  // namespace
 
-// Row-tile height for a launch: the one (256 or 224 rows) with the fewer rows per CU over all rounds of tiles, 256 on
-// a tie; split launches keep 256 (their range count is sized for 256-row tiles).
-int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
+// Row-tile height for a launch: the one (256 or 224 rows) with the fewer rows per CU over all rounds of tiles, 256 on a
+// tie; for decode-shaped passes (`short_segs`: few tokens per adapter segment, where a tile's time goes to streaming
+// its segments' sB rather than to its K loop) 128 rows when that is strictly fewer, e.g. 4096 decode rows through
+// 2048 columns: 128 tiles of 256 rows leave half the CUs idle. Split launches keep 256 (their range count is sized
+// for 256-row tiles).
+int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit, bool short_segs) {
   if (ksplit != 1) return 8;
   static int cus[64] = {};
   int dev = 0;
@@ -596,7 +600,8 @@ int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit) {
     const int64_t tiles = ((tokens + 32 * mb - 1) / (32 * mb)) * n_tiles;
     return ((tiles + cus[dev] - 1) / cus[dev]) * mb;
   };
-  return cost(7) < cost(8) ? 7 : 8;
+  const int best = cost(7) < cost(8) ? 7 : 8;
+  return short_segs && cost(4) < cost(best) ? 4 : best;
 }
 
 int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
@@ -607,15 +612,18 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
   if (inter > 0 && (part != nullptr || inter % 128 || n_out != 2 * inter)) return MLORA_EINVAL;
   const int n_tiles = inter > 0 ? inter / 128 : (n_out + kTN - 1) / kTN;
-  const int mb = tile_blocks(r.tokens, n_tiles, ksplit);
+  const int64_t segs = r.requests < L.pool_rows ? r.requests : L.pool_rows;
+  const int mb = tile_blocks(r.tokens, n_tiles, ksplit, r.tokens < 16 * (segs > 0 ? segs : 1));
   const int m_tiles = (int)((r.tokens + 32 * mb - 1) / (32 * mb));
   const int64_t blocks = (int64_t)m_tiles * n_tiles * ksplit;
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);  // gated: inter % 128 == 0
   const dim3 grid((unsigned)blocks);
-  auto kernel = inter > 0 ? (mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
-                          : (mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
+  auto kernel = inter > 0 ? (mb == 4 ? base_mfma256_kernel<4, true>
+                                     : mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
+                          : (mb == 4 ? base_mfma256_kernel<4, false>
+                                     : mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid,
                      n_tiles, (vec ? kStoreVec : 0) | (residual ? kStoreResidual : 0), part, ksplit, (int32_t)blocks,
                      inter);
