@@ -36,6 +36,7 @@ constexpr int kThreads = 512;
 constexpr int kRankChunk = 64;   // ranks of sB staged per epilogue pass
 constexpr int kXLoads = 4;       // global_load_lds instructions per lane and step
 constexpr int kWLoads = 4 + 2;   // weight loads per lane and step: 4 words, a scale, a zero point
+constexpr int32_t kLoraEarly = 4;  // `vec` bit: odd row tiles add the LoRA term before the K loop
 
 __shared__ __attribute__((aligned(16))) uint16_t g_x0[kTM * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t g_x1[kTM * kTK];
@@ -234,7 +235,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // and bounds, 64 segments at a time) and taken with readlane, with no memory latency per segment; the first two
   // segments' adapters and live ranks of the first matrix were read in the prologue, so a prefill tile (one or two
   // segments) starts its sB loads at once. st0 (and st1, the gated form's second buffer) are the LDS buffers the first
-  // factors are staged in (two of the x ring, idle after the K loop).
+  // factors are staged in: after the K loop any of the ring; before it (`early`) the two the loop writes last (g_x3 is
+  // the output tile's only; g_x2 is first written by the loop's first step, after a barrier).
   auto lora_term = [&](uint16_t* st0, uint16_t* st1) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
@@ -444,6 +446,13 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       }
     }
   };
+  // Decode-shaped passes (kLoraEarly, set by the host for short segments) alternate the term's place by row tile: odd
+  // row tiles add it before their K loop, so while some workgroups stream sB from memory others run their MFMA loops
+  // (all at once, the sB streams of a round of tiles queue at the memory). The order depends on the row tile alone,
+  // and the gated and plain forms of a group cut the same row tiles, so an output's sum is formed in the same order
+  // in both. (Not in 224-row tiles: their scalar registers do not hold both phases' state.)
+  const bool early = MB != 7 && lora && (vec & kLoraEarly) && (mt & 1);
+  if (early) lora_term(g_x3, g_x2);
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
   load_a(g_x0, 0, a);
@@ -496,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     return;
   }
 
-  if (lora) lora_term(g_x0, g_x1);
+  if (lora && !early) lora_term(g_x0, g_x1);
 
   // Single rounding to bf16 and the stores, through LDS (the whole tile at once): lane l holds, for row
   // mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave
@@ -619,13 +628,15 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
   // 16-byte stores of eight columns need 16-byte aligned output rows
   const bool vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0) && y_stride % 8 == 0 && n_out % 8 == 0 &&
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);  // gated: inter % 128 == 0
+  const bool early = part == nullptr && r.tokens < 16 * (segs > 0 ? segs : 1);  // decode-shaped: alternate the order
   const dim3 grid((unsigned)blocks);
   auto kernel = inter > 0 ? (mb == 4 ? base_mfma256_kernel<4, true>
                                      : mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
                           : (mb == 4 ? base_mfma256_kernel<4, false>
                                      : mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid,
-                     n_tiles, (vec ? kStoreVec : 0) | (residual ? kStoreResidual : 0), part, ksplit, (int32_t)blocks,
+                     n_tiles, (vec ? kStoreVec : 0) | (residual ? kStoreResidual : 0) | (early ? kLoraEarly : 0), part,
+                     ksplit, (int32_t)blocks,
                      inter);
   return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }
