@@ -21,8 +21,9 @@
 // arrays chosen at compile time (the loop is unrolled by six). Tiles are ordered so that the column tiles of one
 // row tile run on the same XCD (its x rows, the larger operand, then come from that XCD's L2).
 // Epilogue: the tile's first factors (sorted rows) are staged in LDS; each adapter segment crossing the tile adds
-// its sB rows (loaded straight into operands, one segment ahead) times the first factors of its rows by MFMA; then
-// the single rounding to bf16, staged through LDS so every output row is written in whole 512-byte pieces.
+// its sB rows (loaded straight into operands, segments ahead) times the first factors of its rows by MFMA; then the
+// single rounding to bf16, staged through LDS so every output row is written in whole 512-byte pieces. Decode-shaped
+// passes (few tokens per segment) alternate: odd row tiles add their LoRA term before the K loop.
 #include <type_traits>
 
 #include "tile_common.h"
