@@ -229,8 +229,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   auto half_of = [](uint64_t pair, int i) __attribute__((always_inline)) { return (int)(uint32_t)(pair >> (32 * i)); };
   // LoRA second factor. The tile's rows of the first factor (sorted order, 64 ranks of a matrix at a time) are staged
   // in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come straight from
-  // memory as MFMA operands ahead of their products (three segments in the plain form, one in the gated form, whose
-  // wave-dependent matrix leaves fewer registers), and the products are added with the first
+  // memory as MFMA operands one segment ahead of their products (deeper, the decode-pool groups were 2-7% slower: a
+  // round of tiles' sB streams already queue at the memory), and the products are added with the first
   // factors of rows outside the segment, and ranks past the adapter's live rank, set to zero. A decode-shaped tile
   // crosses ~64 segments, so their bookkeeping is read into lane tables (lane i: segment c0 + i's adapter, live rank
   // and bounds, 64 segments at a time) and taken with readlane, with no memory latency per segment; the first two
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
     // one pass over the segments: `stage` stages the first factors, then per chunk of 64 segments the lane tables
-    // (ta, tb, te: adapter and bounds; tl: live rank of matrix j) and the segments' products, sB three ahead.
+    // (ta, tb, te: adapter and bounds; tl: live rank of matrix j) and the segments' products, sB one ahead.
     // `ahead`: the prologue's read-ahead applies (the first chunk of matrix jlo); `rc` the rank chunk
     auto pass = [&](int j, int rc, bool ahead, auto&& stage, auto&& load_seg, auto&& apply_seg)
         __attribute__((always_inline)) {
@@ -266,8 +266,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             live = __builtin_amdgcn_readlane(tl, i);
           }
         };
-        uint4 q0[4], q1[4], q2[4];
-        int k0, k1, k2;
+        uint4 q0[4], q1[4];
+        int k0, k1;
         auto load = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
           int a, live;
           seg(s, a, live);
@@ -281,19 +281,16 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
           apply_seg(__builtin_amdgcn_readlane(tb, i) - (int)p0, __builtin_amdgcn_readlane(te, i) - (int)p0, bv, rk);
         };
         load(c0, q0, k0);
-        load(c0 + 1, q1, k1);
-        load(c0 + 2, q2, k2);
         if (c0 == s_lo) {
-          MLORA_WAIT_VM(12);  // the staged first factors have landed (the sB loads may be in flight)
+          MLORA_WAIT_VM(4);  // the staged first factors have landed (the sB loads may be in flight)
           lds_sync();
         }
-        for (int s = c0; s <= cend; s += 3) {
+        for (int s = c0; s <= cend; s += 2) {
+          load(s + 1, q1, k1);
           apply(s, q0, k0);
-          load(s + 3, q0, k0);
+          if (s + 1 > cend) break;
+          load(s + 2, q0, k0);
           apply(s + 1, q1, k1);
-          load(s + 4, q1, k1);
-          apply(s + 2, q2, k2);
-          load(s + 5, q2, k2);
         }
       }
     };
