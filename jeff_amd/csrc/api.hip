@@ -167,10 +167,12 @@ int base_of(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r
 
 
 // Input ranges of a narrow product: the forced count, else the count S in {1, 2, 4, 8} (dividing the 64-input steps)
-// with the least estimated time. A workgroup takes about 0.6 us per step plus 12 us of fixed work (loads ahead of the
-// first step, the LoRA term, the stores), in rounds of one per CU; a split adds 2 us (the reduction's launch) and the
-// float32 ranges' round trip through memory at 5 TB/s. (Fitted to 256-token products of 2048 -> 4096, 2048 -> 2048
-// and 6144 -> 2048 columns over 1, 2, 4 and 8 ranges; the estimate picks the fastest count of each: 4, 4 and 8.)
+// with the least estimated time. A base workgroup takes about 0.6 us per step plus 12 us of fixed work, in rounds of
+// one per CU. One range: the first factors' own launch before it (~9 us). S ranges: the expand launch after it
+// (~9 us) and the float32 ranges' round trip through memory, counted at 1 TB/s (the expand's reads of more ranges
+// lengthen its chain). (Fitted to 256-token products of 2048 -> 4096, 2048 -> 2048, gated
+// 2048 -> 2 x 6144 and 6144 -> 2048 columns over 1, 2, 4 and 8 ranges; the estimate picks the fastest count of each:
+// 2, 4, 1 and 4.)
 int32_t narrow_ranges(const mlora_int4_t* w, int32_t flags) {
   if ((flags >> 8) & 0xF) return (flags >> 8) & 0xF;  // forced (base_of checked it)
   const int64_t tiles = w->columns / 64, steps = w->k / 64, cus = device_cus();
@@ -179,8 +181,8 @@ int32_t narrow_ranges(const mlora_int4_t* w, int32_t flags) {
   for (int32_t s = 1; s <= 8; s *= 2) {
     if (steps % s) continue;
     const int64_t rounds = (tiles * s + cus - 1) / cus;
-    double t = (double)rounds * (0.6 * (double)(steps / s) + 12.0);
-    if (s > 1) t += 2.0 + (double)dec_partials_bytes(*w, s) * 2.0 / 5.0e6;
+    const double t = (double)rounds * (0.6 * (double)(steps / s) + 12.0) + 9.0 +
+                     (double)dec_partials_bytes(*w, s) / 1.0e6;
     if (s == 1 || t < best) {
       best = t;
       pick = s;
@@ -210,9 +212,10 @@ size_t partials_of(const mlora_int4_t* w, const mlora_route_t* r, Base base, int
   return base == Base::split ? split_bytes(w, r->tokens) : 0;
 }
 
-// The base product (and the LoRA second factor) once mid holds the first factors.
+// The base product and the LoRA second factor once mid holds the first factors, or, for a narrow product with
+// fuse_shrink, as it computes them (its base launch writes mid).
 int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* r, const uint16_t* x,
-             int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, const uint16_t* mid,
+             int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, uint16_t* mid, bool fuse_shrink,
              void* partials, size_t partials_bytes, Base base, int32_t flags, hipStream_t s) {
   const int32_t inter = gated_width(w, flags);
   const bool resid = residual_of(flags);
@@ -220,8 +223,8 @@ int run_base(const mlora_int4_t* w, const mlora_lora_t* L, const mlora_route_t* 
     const int32_t ks = narrow_ranges(w, flags);
     const size_t need = dec_partials_bytes(*w, ks);
     if (need > 0 && (partials == nullptr || !aligned16(partials) || partials_bytes < need)) return MLORA_EWORKSPACE;
-    return launch_dec(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, static_cast<float*>(partials), ks,
-                      s, inter, resid);
+    return launch_dec(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, fuse_shrink,
+                      static_cast<float*>(partials), ks, s, inter, resid);
   }
   if (base == Base::fused && (inter > 0 || resid))
     return launch_base256(*w, *L, *r, x, x_stride, y, y_stride, last_out, w->out, mid, nullptr, 1, s, inter, resid);
@@ -414,9 +417,12 @@ int mlora_int4_linear(const mlora_int4_t* w, const mlora_lora_t* lora, const mlo
     return launch_finish(*lora, *route, part, ks, w->columns, mid, y, y_stride, last_out, w->out, s,
                          gated_width(w, flags), residual_of(flags));
   }
+  if (base == Base::narrow && !mfma_shrink)  // the segment-form first factors inside the base launch
+    return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, true, partials, partials_bytes, base,
+                    flags, s);
   if ((rc = launch_shrink(*lora, *route, x, x_stride, w->k, mid, mfma_shrink, s))) return rc;
-  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
-                  s);
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, false, partials, partials_bytes, base,
+                  flags, s);
 }
 
 int mlora_int4_linear_noalloc(const mlora_int4_t* w, const mlora_lora_t* lora, const mlora_route_t* route,
@@ -451,8 +457,9 @@ int mlora_int4_base_expand(const mlora_int4_t* w, const mlora_lora_t* lora, cons
     return MLORA_EINVAL;
   Base base;
   if ((rc = base_of(w, lora, route, x_stride, flags, &base))) return rc;
-  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, mid, partials, partials_bytes, base, flags,
-                  static_cast<hipStream_t>(stream));
+  // mid is read only (fuse_shrink false)
+  return run_base(w, lora, route, x, x_stride, y, y_stride, last_out, const_cast<uint16_t*>(mid), false, partials,
+                  partials_bytes, base, flags, static_cast<hipStream_t>(stream));
 }
 
 int mlora_lora_add(const mlora_lora_t* lora, const mlora_route_t* route, const uint16_t* x, int64_t x_stride,

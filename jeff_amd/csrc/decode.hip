@@ -8,16 +8,21 @@
 // each wave reads its 64 rows of x from an LDS ring that buffer loads with the LDS flag fill, as in the prefill kernel;
 // words and x rows are loaded three steps ahead, the step's barrier sits in its middle, so the operand reads of each
 // half of a step overlap the other half's MFMAs, and a step's words are dequantised two steps ahead, past a barrier.
-// When the columns alone are too few for the CUs, the input dimension is split into S ranges: each range writes its
-// float32 tile in the accumulators' own order (one coalesced 1 KB store per MFMA block and column group), and
-// dec_reduce_kernel adds the ranges in order and rounds once.
-// LoRA: the first factors of the wave's rows (64 ranks of matrix j) are loaded once; the adapter segments crossing
-// those rows are listed one per lane (adapter, live rank), and their sB operands stream from memory four segments
-// ahead of the MFMAs (with S input ranges, range ks takes every S-th of the wave's segments from the ks-th). A
-// segment's term goes into the row blocks it crosses, with the first factors of rows outside the segment, and ranks
-// past its live rank, set to zero.
+// One input range (the columns alone fill the CUs): the first factors are computed first (shrink_seg.h, their own
+// launch), and the tile adds the LoRA term after its K loop: the first factors of the wave's rows (64 ranks of matrix
+// j) are loaded before the loop; the adapter segments crossing those rows are listed one per lane (adapter, live
+// rank), and their sB operands stream from memory four segments ahead of the MFMAs. A segment's term goes into the
+// row blocks it crosses, with the first factors of rows outside the segment, and ranks past its live rank, set to
+// zero. The tile is rounded once and written (plain, added to the residual, or silu(gate) * up).
+// S input ranges (the columns alone are too few for the CUs): two launches, neither waiting for another workgroup.
+// The first is the ranges' base tiles, each writing its float32 tile in the accumulators' own order (one coalesced
+// 1 KB store per MFMA block and column group), and, in the workgroups past them, the first factors (one workgroup per
+// (segment, 32-rank block), which read only x and A and so run beside the base tiles: their latency chain overlaps
+// the K loops instead of preceding them). The second, dec_expand_kernel, adds the ranges in order and the LoRA term
+// per (64-row group, column tile), then rounds once and writes.
 #include <type_traits>
 
+#include "shrink_seg.h"
 #include "tile_common.h"
 
 namespace {
@@ -33,10 +38,13 @@ constexpr int kDCols = 32 * kDCG;
 constexpr int kDXLoads = 4;               // x rows: LDS-flag buffer loads per lane and step
 constexpr int kDWLoads = 3;               // weights: a word, a scale and a zero point per thread and step
 constexpr int kDRankChunk = 64;           // ranks of a matrix per LoRA pass
-constexpr int kDRedThreads = 256;
 constexpr int kDMaxRanges = 8;            // input ranges of a narrow product (the host allows 1, 2, 4 or 8)
+constexpr int kESG = 4;                   // the expand launch: segment groups of a row group's segments
+constexpr int kEThreads = 64 * kDCG * kESG;  // one wave per (column group, segment group)
 
 static_assert(kDRows / kDRG == 32 * kDMB, "row groups must cover the tile");
+static_assert(kDThreads == kDWaves * 64, "a first-factor workgroup is a base workgroup's threads");
+static_assert(kDRows * kTK == kSegLds / 2, "a first-factor workgroup stages A in the first two x buffers");
 
 __shared__ __attribute__((aligned(16))) uint16_t d_x0[kDRows * kTK];
 __shared__ __attribute__((aligned(16))) uint16_t d_x1[kDRows * kTK];
@@ -48,21 +56,42 @@ __shared__ uint4 d_w2[8 * kDCols];
 __shared__ int32_t d_orig[kDRows];  // the tile's rows: original token index, -1 past the tokens
 __shared__ int32_t d_last[kDRows];  // the tile's rows: request whose last token it is, else -1
 
-// Float4 index of (range ks, column tile nt, wave, block mb, column group g, lane) in the split partial tiles.
+// Float4 index of (range ks, column tile nt, wave, block mb, column group g, lane) in the partial tiles.
 __device__ __forceinline__ int64_t part_index(int ks, int n_tiles, int nt, int wave, int mb, int g, int lane) {
   return ((((int64_t)ks * n_tiles + nt) * 8 + wave) * kDMB * 4 + mb * 4 + g) * 64 + lane;
 }
 
+// Steps it + B, it + B + 1, ... of a K loop unrolled by 12 (the period of its 4 x buffers and 3 weight buffers), as
+// far as step nk - 1: nested conditions, one exit (a chain of breaks out of the unrolled body compiles to more than the
+// register budget of this kernel).
+template <int B, class F>
+__device__ __forceinline__ void steps_from(F& run, int it, int nk) {
+  run(std::integral_constant<int, B>{}, it + B);
+  if constexpr (B + 1 < 12) {
+    if (it + B + 1 < nk) steps_from<B + 1>(run, it, nk);
+  }
+}
+
 // GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none
-// of it
-template <bool GATED>
+// of it. RANGES false: one range, the LoRA term from mid, the output written. RANGES true: each range's tile goes to
+// part (no LoRA term, no output), and the blocks past the n_tiles x ksplit tiles (the grid's rest) compute the first
+// factors into mid (the tiles come first: they take their CUs at once, and the first-factor blocks, whose LDS share
+// is the tiles' share, fill the remaining CUs); a template parameter so that neither form carries the other's code.
+template <bool GATED, bool RANGES>
 __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
-                                                        const uint16_t* __restrict__ x, int64_t x_stride,
+                                                        const uint16_t* x, int64_t x_stride,
                                                         uint16_t* __restrict__ y, int64_t y_stride,
                                                         uint16_t* __restrict__ last_out, int32_t n_out,
-                                                        const uint16_t* __restrict__ mid, int32_t n_tiles,
-                                                        int32_t vec, float4* __restrict__ part, int32_t ksplit,
-                                                        int32_t inter) {
+                                                        uint16_t* mid, int32_t n_tiles, int32_t vec,
+                                                        float4* __restrict__ part, int32_t ksplit, int32_t inter,
+                                                        int32_t max_blocks) {
+  if constexpr (RANGES) {
+    const int sb = (int)blockIdx.x - n_tiles * ksplit;  // a first-factor block: one of max_segs x max_blocks
+    if (sb >= 0) {
+      shrink_seg_block(L, r, x, x_stride, w.k, mid, max_blocks, sb, d_x0, d_x1);
+      return;
+    }
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses of the x loads in SGPRs
   const int cg = wave % kDCG, rg = wave / kDCG;
@@ -184,7 +213,7 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   // columns (ranks 0..63); the segments' adapters and live ranks follow once the segment range is known.
   const int cw0 = GATED ? (cg ? inter : 0) + nt * 32 : n0 + cg * 32;  // the wave's first column
   const int r_end = min(R0 + 32 * kDMB, T);
-  const bool lora = L.n_mats > 0 && mid != nullptr && cw0 < n_out && R0 < r_end;
+  const bool lora = !RANGES && L.n_mats > 0 && mid != nullptr && cw0 < n_out && R0 < r_end;
   const int jlo = lora ? matrix_of(L, cw0) : 0;
   int rseg[kDMB];
   uint4 m0[kDMB][4];
@@ -267,40 +296,25 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
     // landed: step i + 2's words (its x rows and step i + 3's loads in flight)
     MLORA_WAIT_VM(kDXLoads + kDWLoads + kDXLoads);
     dequant_to(wfar, wdq);
+    // after the first step, the segments' adapters have landed: their live ranks land during the next steps
+    if constexpr (B == 0 && !RANGES)
+      if (i == 0 && lora) llive0 = la == 0 ? 0 : live_rank(L, la, jlo);
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  for (int it = 0; it < nk; it += 12) {
-    run(I0{}, it);
-    if (it == 0 && lora) llive0 = la == 0 ? 0 : live_rank(L, la, jlo);  // lands during the next steps
-    if (it + 1 >= nk) break;
-    run(I1{}, it + 1);
-    if (it + 2 >= nk) break;
-    run(I2{}, it + 2);
-    if (it + 3 >= nk) break;
-    run(I3{}, it + 3);
-    if (it + 4 >= nk) break;
-    run(std::integral_constant<int, 4>{}, it + 4);
-    if (it + 5 >= nk) break;
-    run(std::integral_constant<int, 5>{}, it + 5);
-    if (it + 6 >= nk) break;
-    run(std::integral_constant<int, 6>{}, it + 6);
-    if (it + 7 >= nk) break;
-    run(std::integral_constant<int, 7>{}, it + 7);
-    if (it + 8 >= nk) break;
-    run(std::integral_constant<int, 8>{}, it + 8);
-    if (it + 9 >= nk) break;
-    run(std::integral_constant<int, 9>{}, it + 9);
-    if (it + 10 >= nk) break;
-    run(std::integral_constant<int, 10>{}, it + 10);
-    if (it + 11 >= nk) break;
-    run(std::integral_constant<int, 11>{}, it + 11);
-  }
+  for (int it = 0; it < nk; it += 12) steps_from<0>(run, it, nk);
   MLORA_WAIT_VM(0);
 
-  // LoRA second factor: this range's share of the segments s_lo..s_hi crossing the wave's rows
+  if constexpr (RANGES) {
+    // this range's float32 tile, in the accumulators' order
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        part[part_index(ks, n_tiles, nt, wave, mb, g, lane)] =
+            make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+    return;
+  }
+
+  // LoRA second factor: the segments s_lo..s_hi crossing the wave's rows
   if (lora) {
     const int cc = cw0 + (lane & 31);
     const int jhi = matrix_of(L, min(cw0 + 31, n_out - 1));
@@ -366,12 +380,10 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
           };
           uint4 q0[4], q1[4], q2[4], q3[4];
           int k0, k1, k2, k3;
-          // input range ks takes segments s_lo + ks, s_lo + ks + S, ... (the ranges' sums are added afterwards)
-          const int S = ksplit;
-          load_b(s_lo + ks, q0, k0);
-          load_b(s_lo + ks + S, q1, k1);
-          load_b(s_lo + ks + 2 * S, q2, k2);
-          load_b(s_lo + ks + 3 * S, q3, k3);
+          load_b(s_lo, q0, k0);
+          load_b(s_lo + 1, q1, k1);
+          load_b(s_lo + 2, q2, k2);
+          load_b(s_lo + 3, q3, k3);
           // Each row's first factors past its own segment's live rank are set to zero once, while the first segments'
           // sB loads are in flight (the segment's live rank from its lane of llive, or from memory past the wave's
           // first 64 segments; rows past the pass have none): a segment's term then needs only a row mask on the first
@@ -390,31 +402,21 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             for (int k16 = 0; k16 < 4; ++k16)
               m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
           }
-          for (int s = s_lo + ks; s <= s_hi; s += 4 * S) {
+          for (int s = s_lo; s <= s_hi; s += 4) {
             apply(s, q0, k0);
-            load_b(s + 4 * S, q0, k0);
-            apply(s + S, q1, k1);
-            load_b(s + 5 * S, q1, k1);
-            apply(s + 2 * S, q2, k2);
-            load_b(s + 6 * S, q2, k2);
-            apply(s + 3 * S, q3, k3);
-            load_b(s + 7 * S, q3, k3);
+            load_b(s + 4, q0, k0);
+            apply(s + 1, q1, k1);
+            load_b(s + 5, q1, k1);
+            apply(s + 2, q2, k2);
+            load_b(s + 6, q2, k2);
+            apply(s + 3, q3, k3);
+            load_b(s + 7, q3, k3);
           }
         }
       }
     }
   }
 
-  if (ksplit > 1) {
-    // this range's float32 tile, in the accumulators' order
-#pragma unroll
-    for (int mb = 0; mb < kDMB; ++mb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        part[part_index(ks, n_tiles, nt, wave, mb, g, lane)] =
-            make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
-    return;
-  }
   if constexpr (GATED) {
     // gated, one range: the up waves leave their rounded outputs in LDS (the x ring is idle after the K loop); each
     // gate wave pairs them with its own, lane for lane, and writes silu(gate) * up to output columns 32 nt .. +31
@@ -476,101 +478,267 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   }
 }
 
-// Second launch of a split decode product: thread f takes float4 f of every range's partial tiles (the same position
-// in each), adds the ranges in order, rounds once and writes its row's four columns.
-__global__ __launch_bounds__(kDRedThreads) void dec_reduce_kernel(const float4* __restrict__ part, int32_t ksplit,
-                                                                  int32_t n_tiles, mlora_route_t r,
-                                                                  uint16_t* __restrict__ y, int64_t y_stride,
-                                                                  uint16_t* __restrict__ last_out, int32_t n_out,
-                                                                  int32_t vec) {
-  const int64_t per = (int64_t)n_tiles * 8 * kDMB * 4 * 64;  // float4s per range
-  const int64_t f = (int64_t)blockIdx.x * kDRedThreads + threadIdx.x;
-  if (f >= per) return;
-  const int lane = (int)(f & 63);
-  const int64_t q = f >> 6;
-  const int g = (int)(q & 3), mb = (int)((q >> 2) % kDMB);
-  const int64_t wt = (q >> 2) / kDMB;
-  const int wave = (int)(wt % 8), nt = (int)(wt / 8);
-  const int row = (wave / kDCG) * 32 * kDMB + mb * 32 + (lane & 31);
-  const int col = nt * kDCols + (wave % kDCG) * 32 + g * 8 + (lane >> 5) * 4;
-  if (row >= r.tokens || col >= n_out) return;
-  // every range's float4, then the row's token order, are loaded before the first add (one memory latency, not one
-  // per range), then the ranges are added in order
-  float4 u[kDMaxRanges];
-#pragma unroll
-  for (int ks = 0; ks < kDMaxRanges; ++ks)
-    if (ks < ksplit) u[ks] = part[(int64_t)ks * per + f];
-  const int64_t orig = r.tok_perm[row];
-  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
-  float4 v = u[0];
-#pragma unroll
-  for (int ks = 1; ks < kDMaxRanges; ++ks)
-    if (ks < ksplit) {
-      v.x += u[ks].x;
-      v.y += u[ks].y;
-      v.z += u[ks].z;
-      v.w += u[ks].w;
-    }
-  store4(y + orig * y_stride + col, lq >= 0 ? last_out + lq * n_out + col : nullptr, pack_bf16x2(v.x, v.y),
-         pack_bf16x2(v.z, v.w), n_out - col, vec);
-}
+// The expand launch: block b is (row group b % rgs, column tile b / rgs), rgs = the row groups holding tokens. Wave
+// (cg, sg) covers the base launch's wave (row group, cg), its 64 rows x 32 columns, for the segments s_lo + sg,
+// s_lo + sg + 4, ... crossing those rows, so a wave's few segments' sB loads are in flight at once. A row gets a LoRA
+// term from its own segment only (the others' first factors are masked to zero), so the four groups' sums are exact
+// zeros but for one: group 0 starts from the ranges' sum, groups 1-3 from zero, and they are added in group order
+// through LDS. GATED: silu(gate) * up to inter columns.
+template <bool GATED>
+__global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, mlora_route_t r,
+                                                               const uint16_t* __restrict__ mid,
+                                                               const float4* __restrict__ part, int32_t ksplit,
+                                                               int32_t n_tiles, int32_t rgs,
+                                                               uint16_t* __restrict__ y, int64_t y_stride,
+                                                               uint16_t* __restrict__ last_out, int32_t n_out,
+                                                               int32_t vec, int32_t inter) {
+  __shared__ float e_red[(kESG - 1) * kDCG * kDMB * 16 * 64];  // segment groups 1..3: their sums
+  __shared__ uint2 ex[kDCG * kDMB * 4 * 64];                     // gated: the gate and up waves' rounded outputs
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ew = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = ew % kDCG, sg = ew / kDCG;
+  const int rg = blockIdx.x % rgs, nt = blockIdx.x / rgs;
+  const int wave = rg * kDCG + cg;  // the base launch's wave of these rows and columns
+  const int T = (int)r.tokens;
+  const int R0 = rg * 32 * kDMB;
+  const int r_end = min(R0 + 32 * kDMB, T);  // R0 < T: rgs row groups hold tokens
+  const int cw0 = GATED ? (cg ? inter : 0) + nt * 32 : nt * kDCols + cg * 32;  // the wave's first column
+  const bool lora = L.n_mats > 0 && cw0 < n_out;
 
-// The same for a gated product: thread f takes float4 f of the gate waves' partial tiles (column group 0 of every row
-// group) and the matching float4 of the up waves' (column group 1), adds each over the ranges in order, rounds both
-// and writes silu(gate) * up to its row's four output columns 32 nt + 8 g + 4 (lane >> 5) .. +3.
-__global__ __launch_bounds__(kDRedThreads) void dec_reduce_gated_kernel(const float4* __restrict__ part,
-                                                                        int32_t ksplit, int32_t n_tiles,
-                                                                        mlora_route_t r, uint16_t* __restrict__ y,
-                                                                        int64_t y_stride,
-                                                                        uint16_t* __restrict__ last_out,
-                                                                        int32_t inter, int32_t vec) {
-  const int64_t per = (int64_t)n_tiles * 8 * kDMB * 4 * 64;  // float4s per range
-  const int64_t f = (int64_t)blockIdx.x * kDRedThreads + threadIdx.x;
-  if (f >= per / 2) return;
-  const int lane = (int)(f & 63);
-  const int64_t q = f >> 6;
-  const int g = (int)(q & 3), mb = (int)((q >> 2) % kDMB);
-  const int64_t t2 = (q >> 2) / kDMB;
-  const int rg = (int)(t2 % kDRG), nt = (int)(t2 / kDRG);
-  const int row = rg * 32 * kDMB + mb * 32 + (lane & 31);
-  const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
-  if (row >= r.tokens) return;
-  const int64_t fg = part_index(0, n_tiles, nt, rg * kDCG, mb, g, lane);
-  const int64_t fu = part_index(0, n_tiles, nt, rg * kDCG + 1, mb, g, lane);
-  // all loads first (every range's gate and up float4s, then the row's token order), then the ranges added in order
-  float4 a[kDMaxRanges], b[kDMaxRanges];
+  // first factors of the wave's rows R0 + 32 mb + (lane & 31), ranks rc + 16 k16 + 8 (lane >> 5) .. +7 of matrix j
+  // (zero past the pass's rows and past cap_j)
+  auto load_mid = [&](uint4 (&m)[kDMB][4], int j, int rc) __attribute__((always_inline)) {
+    const int capj = L.cap[j], rho = rank_offset(L, j);
 #pragma unroll
-  for (int ks = 0; ks < kDMaxRanges; ++ks)
-    if (ks < ksplit) {
-      a[ks] = part[(int64_t)ks * per + fg];
-      b[ks] = part[(int64_t)ks * per + fu];
-    }
-  const int64_t orig = r.tok_perm[row];
-  const int64_t lq = last_out != nullptr ? r.last_of[row] : -1;
-  float4 gv = a[0], uv = b[0];
+    for (int mb = 0; mb < kDMB; ++mb)
 #pragma unroll
-  for (int ks = 1; ks < kDMaxRanges; ++ks)
-    if (ks < ksplit) {
-      gv.x += a[ks].x;
-      gv.y += a[ks].y;
-      gv.z += a[ks].z;
-      gv.w += a[ks].w;
-      uv.x += b[ks].x;
-      uv.y += b[ks].y;
-      uv.z += b[ks].z;
-      uv.w += b[ks].w;
+      for (int k16 = 0; k16 < 4; ++k16) {
+        const int row = R0 + mb * 32 + (lane & 31);
+        const int q = rc + 16 * k16 + 8 * (lane >> 5);
+        m[mb][k16] = (row < r_end && q < capj)
+                         ? *reinterpret_cast<const uint4*>(mid + (int64_t)row * L.rank_cap + rho + q)
+                         : make_uint4(0, 0, 0, 0);
+      }
+  };
+
+  // Everything that depends on no other load is issued first, in one round: each lane's row of block mb and that
+  // row's segment (-1 past the pass), the first factors of the wave's rows for the first matrix of its columns
+  // (ranks 0..63), the rows' token order for the output (group 0), the ranges' tiles (group 0). Then the two
+  // dependent rounds of bookkeeping: per block, the segments it crosses, and the wave's segments (at most 64: one per
+  // row), one per lane: its adapter; then the adapters' live ranks.
+  const int jlo = lora ? matrix_of(L, cw0) : 0;
+  int rseg[kDMB], blo[kDMB], bhi[kDMB], s_lo = 0, s_hi = -1, la = 0, llive0 = 0;
+  uint4 m0[kDMB][4];
+  if (lora) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) {
+      const int row = R0 + mb * 32 + (lane & 31);
+      rseg[mb] = row < r_end ? r.seg_of[row] : -1;
     }
-  const uint2 v = silu_mul4(make_uint2(pack_bf16x2(gv.x, gv.y), pack_bf16x2(gv.z, gv.w)),
-                            make_uint2(pack_bf16x2(uv.x, uv.y), pack_bf16x2(uv.z, uv.w)));
-  const uint32_t lo = v.x, hi = v.y;
-  if (vec & kStoreVec) {
-    *reinterpret_cast<uint2*>(y + orig * y_stride + col) = make_uint2(lo, hi);
-    if (lq >= 0) *reinterpret_cast<uint2*>(last_out + lq * inter + col) = make_uint2(lo, hi);
-  } else {
-    const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
-    for (int e = 0; e < 4; ++e) {
-      y[orig * y_stride + col + e] = h[e];
-      if (lq >= 0) last_out[lq * inter + col + e] = h[e];
+    load_mid(m0, jlo, 0);
+  }
+  int64_t orig[kDMB], lq[kDMB];
+#pragma unroll
+  for (int mb = 0; mb < kDMB; ++mb) {
+    const int row = R0 + mb * 32 + (lane & 31);
+    orig[mb] = sg == 0 && row < T ? r.tok_perm[row] : 0;
+    lq[mb] = sg == 0 && row < T && last_out != nullptr ? r.last_of[row] : -1;
+  }
+
+  // segment group 0: the ranges' tiles added in order, four ranges' loads in flight at a time
+  f32x16_t acc[kDMB];
+#pragma unroll
+  for (int mb = 0; mb < kDMB; ++mb) acc[mb] = f32x16_t{};
+  for (int k0 = 0; k0 < (sg == 0 ? ksplit : 0); k0 += 4) {
+    float4 u[4][kDMB * 4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (k0 + i < ksplit)
+#pragma unroll
+        for (int e = 0; e < kDMB * 4; ++e) u[i][e] = part[part_index(k0 + i, n_tiles, nt, wave, e / 4, e % 4, lane)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (k0 + i < ksplit)
+#pragma unroll
+        for (int e = 0; e < kDMB * 4; ++e) {
+          const int mb = e / 4, g = e % 4;
+          if (k0 + i == 0) {
+            acc[mb][4 * g] = u[i][e].x;
+            acc[mb][4 * g + 1] = u[i][e].y;
+            acc[mb][4 * g + 2] = u[i][e].z;
+            acc[mb][4 * g + 3] = u[i][e].w;
+          } else {
+            acc[mb][4 * g] += u[i][e].x;
+            acc[mb][4 * g + 1] += u[i][e].y;
+            acc[mb][4 * g + 2] += u[i][e].z;
+            acc[mb][4 * g + 3] += u[i][e].w;
+          }
+        }
+  }
+
+  if (lora) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) {
+      const int last = r_end - 1 - (R0 + mb * 32);  // the block's last row in the pass, relative to its first
+      blo[mb] = last >= 0 ? __builtin_amdgcn_readfirstlane(rseg[mb]) : INT_MAX;
+      bhi[mb] = last >= 0 ? __builtin_amdgcn_readlane(rseg[mb], min(last, 31)) : -1;
+    }
+    s_lo = blo[0];
+    s_hi = bhi[kDMB - 1] >= 0 ? bhi[kDMB - 1] : bhi[0];
+    la = s_lo + lane <= s_hi ? r.seg_adapter[s_lo + lane] : 0;
+    llive0 = la == 0 ? 0 : live_rank(L, la, jlo);
+  }
+
+  // LoRA second factor: the wave's share of the segments s_lo..s_hi crossing its rows
+  if (lora) {
+    const int cc = cw0 + (lane & 31);
+    const int jhi = matrix_of(L, min(cw0 + 31, n_out - 1));
+    for (int j = jlo; j <= jhi; ++j) {
+      const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j];
+      const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
+      const bool allin = cw0 >= oj && cw0 + 32 <= oj + cj && cw0 + 32 <= n_out;  // every lane's column in matrix j
+      const int ccol = (cin ? cc : oj) - oj;
+      const int llive = j == jlo ? llive0 : (la == 0 ? 0 : live_rank(L, la, j));
+      for (int rc = 0; rc < capj; rc += kDRankChunk) {
+        uint4 m[kDMB][4];
+        if (j == jlo && rc == 0) {
+#pragma unroll
+          for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) m[mb][k16] = m0[mb][k16];
+        } else {
+          load_mid(m, j, rc);
+        }
+        // sB operands of segment s (ranks rc + 16 k16 + 8 (lane >> 5) .. +7): unconditional loads inside the
+        // adapter's block (clamped to its last 8 ranks), masked when used
+        // The wave's first 64 segments are held one per lane; empty segments (requests of no tokens) can put more
+        // than 64 segment indices across its 64 rows, and those past the 64th are read from memory (i is uniform).
+        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+          const int sc = min(s, s_hi), i = sc - s_lo;
+          int a, live;
+          if (i < kWave) {
+            a = __builtin_amdgcn_readlane(la, i);
+            live = __builtin_amdgcn_readlane(llive, i);
+          } else {
+            a = r.seg_adapter[sc];
+            live = a == 0 ? 0 : live_rank(L, a, j);
+          }
+          rk = s <= s_hi ? min(live - rc, kDRankChunk) : 0;
+          const int sbs = sb_stride(live, capj);  // at least 8: capj > rc >= 0
+          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
+            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+          }
+        };
+        auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+          if (rk <= 0) return;
+          uint32_t rmask[kDMB];
+#pragma unroll
+          for (int mb = 0; mb < kDMB; ++mb) rmask[mb] = rseg[mb] == s ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) {
+            if (16 * k16 >= rk) break;
+            uint4 bm = bv[k16];
+            if (16 * k16 + 16 > rk) bm = keep_first(bm, rk - (16 * k16 + 8 * (lane >> 5)));
+            if (!allin) bm = cin ? bm : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < kDMB; ++mb) {
+              if (s < blo[mb] || s > bhi[mb]) continue;
+              const uint4 am = make_uint4(m[mb][k16].x & rmask[mb], m[mb][k16].y & rmask[mb],
+                                          m[mb][k16].z & rmask[mb], m[mb][k16].w & rmask[mb]);
+              acc[mb] = mfma32(bm, am, acc[mb]);
+            }
+          }
+        };
+        uint4 q0[4], q1[4];
+        int k0, k1;
+        load_b(s_lo + sg, q0, k0);
+        load_b(s_lo + sg + kESG, q1, k1);
+        // Each row's first factors past its own segment's live rank are set to zero once, while the first segments'
+        // sB loads are in flight (the segment's live rank from its lane of llive, or from memory past the wave's
+        // first 64 segments; rows past the pass have none): a segment's term then needs only a row mask on the first
+        // factors, and the sB chunk crossing the live rank (rk not a multiple of 16) keeps only its live ranks, so
+        // the sB row's padding never enters the sum.
+#pragma unroll
+        for (int mb = 0; mb < kDMB; ++mb) {
+          const int sq = rseg[mb] - s_lo;
+          int rrow = __builtin_amdgcn_ds_bpermute((sq & 63) << 2, llive);
+          if (rseg[mb] >= 0 && sq >= kWave) {
+            const int a = r.seg_adapter[rseg[mb]];
+            rrow = a == 0 ? 0 : live_rank(L, a, j);
+          }
+          if (rseg[mb] < 0) rrow = 0;
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16)
+            m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
+        }
+        for (int s = s_lo + sg; s <= s_hi; s += 2 * kESG) {
+          apply(s, q0, k0);
+          load_b(s + 2 * kESG, q0, k0);
+          apply(s + kESG, q1, k1);
+          load_b(s + 3 * kESG, q1, k1);
+        }
+      }
+    }
+  }
+
+  // segment groups 1..3 hand their sums to group 0, which adds them in order
+  float* red = e_red + (size_t)((sg - 1) * kDCG + cg) * (kDMB * 16 * 64);
+  if (sg > 0) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) red[(mb * 16 + i) * 64 + lane] = acc[mb][i];
+  }
+  lds_sync();
+  if (sg == 0) {
+    for (int g = 1; g < kESG; ++g) {
+      const float* rg_sum = e_red + (size_t)((g - 1) * kDCG + cg) * (kDMB * 16 * 64);
+#pragma unroll
+      for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mb][i] += rg_sum[(mb * 16 + i) * 64 + lane];
+    }
+  }
+  if constexpr (GATED) {
+    // the gate and up waves leave their rounded outputs in LDS; then wave cg pairs gate and up of row block cg, lane
+    // for lane, and writes silu(gate) * up to output columns 32 nt .. +31
+    static_assert(kDMB == kDCG, "one row block per column group's wave");
+    if (sg == 0) {
+#pragma unroll
+      for (int mb = 0; mb < kDMB; ++mb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          ex[((cg * kDMB + mb) * 4 + g) * 64 + lane] = make_uint2(pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]),
+                                                                  pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]));
+    }
+    lds_sync();
+    const int mb = cg, row = R0 + mb * 32 + (lane & 31);
+    if (sg != 0 || row >= T) return;
+    const int64_t o = cg == 0 ? orig[0] : orig[1], q = cg == 0 ? lq[0] : lq[1];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint2 v = silu_mul4(ex[(mb * 4 + g) * 64 + lane], ex[((kDMB + mb) * 4 + g) * 64 + lane]);
+      const int col = nt * 32 + g * 8 + (lane >> 5) * 4;
+      store4(y + o * y_stride + col, q >= 0 ? last_out + q * inter + col : nullptr, v.x, v.y, 4, vec & kStoreVec);
+    }
+    return;
+  }
+  // round once and write four columns per lane and group (rows in their original order)
+  if (sg != 0) return;
+#pragma unroll
+  for (int mb = 0; mb < kDMB; ++mb) {
+    const int row = R0 + mb * 32 + (lane & 31);
+    if (row >= T) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = cw0 + g * 8 + (lane >> 5) * 4;
+      if (col >= n_out) continue;
+      store4(y + orig[mb] * y_stride + col, lq[mb] >= 0 ? last_out + lq[mb] * n_out + col : nullptr,
+             pack_bf16x2(acc[mb][4 * g], acc[mb][4 * g + 1]), pack_bf16x2(acc[mb][4 * g + 2], acc[mb][4 * g + 3]),
+             n_out - col, vec);
     }
   }
 }
@@ -583,8 +751,8 @@ size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit) {
 }
 
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
-               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter, bool residual) {
+               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out, uint16_t* mid,
+               bool shrink, float* part, int32_t ksplit, hipStream_t stream, int32_t inter, bool residual) {
   if (r.tokens == 0 || n_out == 0) return MLORA_OK;
   if (ksplit < 1 || ksplit > kDMaxRanges) return MLORA_EINVAL;
   if (r.tokens > kDRows || w.columns % kDCols || (w.k / kTK) % ksplit || (residual && inter > 0)) return MLORA_EINVAL;
@@ -598,22 +766,35 @@ int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t
                            ? kStoreVec
                            : 0) |
                       (residual ? kStoreResidual : 0);
-  float4* p4 = reinterpret_cast<float4*>(part);
-  hipLaunchKernelGGL(inter > 0 ? dec_kernel<true> : dec_kernel<false>, dim3((unsigned)(n_tiles * ksplit)),
-                     dim3(kDThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, n_tiles,
-                     vec, p4, ksplit, inter);
-  if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
-  if (ksplit > 1) {
-    const int64_t per = (int64_t)n_tiles * kDRows * kDCols / 4;
-    if (inter > 0)
-      hipLaunchKernelGGL(dec_reduce_gated_kernel, dim3((unsigned)((per / 2 + kDRedThreads - 1) / kDRedThreads)),
-                         dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, inter,
-                         vec);
-    else
-      hipLaunchKernelGGL(dec_reduce_kernel, dim3((unsigned)((per + kDRedThreads - 1) / kDRedThreads)),
-                         dim3(kDRedThreads), 0, stream, p4, ksplit, n_tiles, r, y, y_stride, last_out, n_out,
-                         vec);
-    if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
+  if (ksplit == 1) {
+    // the first factors, then the tiles with the LoRA term
+    if (shrink) {
+      const int rc = launch_shrink(L, r, x, x_stride, w.k, mid, false, stream);
+      if (rc) return rc;
+    }
+    hipLaunchKernelGGL((inter > 0 ? dec_kernel<true, false> : dec_kernel<false, false>), dim3((unsigned)n_tiles),
+                       dim3(kDThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid, n_tiles,
+                       vec, nullptr, 1, inter, 0);
+    return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
   }
-  return MLORA_OK;
+  // first-factor blocks: every (segment, 32-rank block) pair of the route's capacity
+  int max_blocks = 0;
+  for (int j = 0; j < L.n_mats; ++j) max_blocks += (L.cap[j] + 31) / 32;
+  const int64_t shrink_blocks = shrink ? (int64_t)r.max_segs * max_blocks : 0;
+  if (shrink_blocks + (int64_t)n_tiles * ksplit > INT_MAX) return MLORA_EOVERFLOW;
+  float4* p4 = reinterpret_cast<float4*>(part);
+  hipLaunchKernelGGL((inter > 0 ? dec_kernel<true, true> : dec_kernel<false, true>),
+                     dim3((unsigned)(shrink_blocks + n_tiles * ksplit)), dim3(kDThreads), 0, stream, w, L, r, x,
+                     x_stride, y, y_stride, last_out, n_out, mid, n_tiles, vec, p4, ksplit, inter,
+                     max_blocks);
+  if (hipGetLastError() != hipSuccess) return MLORA_ELAUNCH;
+  const int rgs = (int)((r.tokens + 32 * kDMB - 1) / (32 * kDMB));  // row groups holding tokens
+  const dim3 grid((unsigned)(n_tiles * rgs));
+  if (inter > 0)
+    hipLaunchKernelGGL(dec_expand_kernel<true>, grid, dim3(kEThreads), 0, stream, L, r, mid, p4, ksplit, n_tiles,
+                       rgs, y, y_stride, last_out, n_out, vec, inter);
+  else
+    hipLaunchKernelGGL(dec_expand_kernel<false>, grid, dim3(kEThreads), 0, stream, L, r, mid, p4, ksplit, n_tiles,
+                       rgs, y, y_stride, last_out, n_out, vec, inter);
+  return hipGetLastError() == hipSuccess ? MLORA_OK : MLORA_ELAUNCH;
 }

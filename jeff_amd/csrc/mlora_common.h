@@ -240,12 +240,15 @@ bool finish_registers(const mlora_lora_t& L);
 int launch_finish(const mlora_lora_t& L, const mlora_route_t& r, const float* part, int32_t ksplit, int32_t ld,
                   const uint16_t* mid, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
                   hipStream_t stream, int32_t inter = 0, bool residual = false);
-// Narrow product (every token, at most 256, in one row tile of 64 columns): ksplit input ranges; with ksplit > 1
-// part holds dec_partials_bytes(w, ksplit) and a second launch adds the ranges (residual as above, not gated).
+// Narrow product (every token, at most 256, in one row tile of 64 columns; inter and residual as above). One input
+// range: the tiles add the LoRA term themselves. ksplit > 1 ranges: float32 tiles in part (dec_partials_bytes(w,
+// ksplit)), then a second launch adds the ranges and the LoRA term. shrink: the product computes the first factors
+// into mid (segment form: their own launch before one range, inside the first launch with ranges); else mid holds
+// them.
 size_t dec_partials_bytes(const mlora_int4_t& w, int32_t ksplit);
 int launch_dec(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
-               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,
-               const uint16_t* mid, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
+               int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out, uint16_t* mid,
+               bool shrink, float* part, int32_t ksplit, hipStream_t stream, int32_t inter = 0,
                bool residual = false);
 int launch_base(const mlora_int4_t* w, const mlora_lora_t& L, const mlora_route_t& r, const uint16_t* x,
                 int64_t x_stride, uint16_t* y, int64_t y_stride, uint16_t* last_out, int32_t n_out,

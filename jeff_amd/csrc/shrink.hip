@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kDWaves * 64) void shrink_seg_kernel(mlora_lora_t L
                                                                  int32_t k, uint16_t* __restrict__ mid,
                                                                  int32_t max_blocks) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[kSegLds];
-  shrink_seg_block(L, r, x, x_stride, k, mid, max_blocks, blockIdx.x, lds);
+  shrink_seg_block(L, r, x, x_stride, k, mid, max_blocks, blockIdx.x, lds, lds + kSegLds / 2);
 }
 
 }  // namespace

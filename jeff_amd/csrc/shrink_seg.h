@@ -19,6 +19,7 @@ __device__ __forceinline__ void rank_block(const int* rk, int n_mats, int b, int
 constexpr int kDWaves = 8;                // waves per workgroup of the segment form, each a share of the inputs
 constexpr int kDChunk = 64;               // inputs per staged chunk of A (32 rank rows of 128 bytes)
 constexpr int kSegLds = kDWaves * 2 * 32 * kDChunk;  // bf16 elements of LDS: two chunk buffers per wave
+static_assert(kDWaves * 16 * kWave * 2 <= kSegLds / 2, "the waves' sums fit the first half of the LDS");
 
 // Short segments (decode): one workgroup per (segment, 32-rank block of a matrix's capacity); blocks past the
 // adapter's live rank of that matrix return at once. Its 8 waves split the input dimension into chunks of 64. A wave
@@ -29,12 +30,13 @@ constexpr int kSegLds = kDWaves * 2 * 32 * kDChunk;  // bf16 elements of LDS: tw
 // sums are then added in wave order through LDS and rounded once. Segments longer than 32 rows take their rows 32 at
 // a time (A is then re-read from L2). The block's bookkeeping is read in two dependent rounds (segment bounds and
 // adapter together, then the adapter's rank and the segment's token order) before the A and x loads. `block` is the
-// workgroup's index among the (segment, rank block) pairs, `lds` kSegLds elements of LDS. Every thread of the
+// workgroup's index among the (segment, rank block) pairs; `lds_lo` and `lds_hi` are kSegLds / 2 elements of LDS
+// each (waves 0-3 stage A in the first, waves 4-7 in the second; the waves' sums use the first). Every thread of the
 // workgroup must call it (it synchronises the workgroup).
 __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const mlora_route_t& r,
                                                  const uint16_t* x, int64_t x_stride, int32_t k,
                                                  uint16_t* __restrict__ mid, int32_t max_blocks, int block,
-                                                 uint16_t* __restrict__ lds) {
+                                                 uint16_t* __restrict__ lds_lo, uint16_t* __restrict__ lds_hi) {
   const int s = block / max_blocks;
   int j = 0, kb = block - s * max_blocks;  // (matrix, 32-rank block) from the capacities
   while (j + 1 < L.n_mats && kb >= (L.cap[j] + 31) >> 5) {
@@ -68,7 +70,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
     const int row = 8 * i + (lane >> 3);
     aoff[i] = (uint32_t)(((row < live_rows ? row : 0) * k + (swz_slot(row, lane & 7) << 3)) * 2);
   }
-  uint16_t* buf0 = lds + wave * (2 * 32 * kDChunk);
+  uint16_t* buf0 = (wave < kDWaves / 2 ? lds_lo : lds_hi) + (wave % (kDWaves / 2)) * (2 * 32 * kDChunk);
   uint16_t* buf1 = buf0 + 32 * kDChunk;
   auto dma_a = [&](uint16_t* buf, int kc) __attribute__((always_inline)) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are done
@@ -78,7 +80,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
   };
   const int chunks = k / kDChunk;
   const int ch0 = (wave * chunks) / kDWaves, ch1 = ((wave + 1) * chunks) / kDWaves;  // this wave's chunks
-  float* red = reinterpret_cast<float*>(lds);
+  float* red = reinterpret_cast<float*>(lds_lo);  // 8 waves x 16 x 64 floats: kSegLds / 2 elements
   for (int64_t p0 = sb; p0 < se; p0 += 32) {
     const int64_t prow = p0 + (lane & 31);
     const bool rin = prow < se;
