@@ -335,8 +335,9 @@ def measure(name: str, steps: int, warmup: int, kernel_reps: int, headline: bool
               "base_mfma_kernel<true> (INT4 base + fused LoRA expand)",
               "split": f"base_mfma256_kernel, split mode ({ranges} input ranges) + "
                        f"{'finish_gated_kernel' if gated else 'finish_kernel'} (INT4 base + LoRA expand{fin})",
-              "narrow": f"dec_kernel (INT4 base + fused LoRA expand{fin}; {ranges} input ranges"
-                        + (", added by dec_reduce_kernel)" if ranges > 1 else ")"),
+              "narrow": (f"dec_kernel (INT4 base, {ranges} input ranges) + dec_expand_kernel (the ranges' sum + "
+                         f"LoRA expand{fin})" if ranges > 1 else f"dec_kernel (INT4 base + fused LoRA expand{fin}; "
+                                                                 f"1 input range)"),
               "gemv": "base_gemv_kernel<true> (INT4 base + fused LoRA expand)"}[base]
     roof.update({"kernel": kernel, "group": f"layer0.{DOMINANT}", "launch_ms": kms, "reps": reps,
                  "route_ms_subtracted": route_ms, "flops_per_launch": kflops, "bytes_per_launch": kbytes})
