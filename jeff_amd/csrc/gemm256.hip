@@ -64,7 +64,18 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // row tile and K range) are consecutive and so run on one XCD.
   const int b = xcd_tile(blockIdx.x, base_blocks);
   const int t = b % (base_blocks / ksplit), ks = b / (base_blocks / ksplit);
-  const int mt = t / n_tiles, nt = t - mt * n_tiles;
+  // Decode-shaped passes (kLoraEarly) take the row tiles in pairs, column tiles interleaved (2m, 0), (2m + 1, 0),
+  // (2m, 1), ...: the two tiles of a pair add their LoRA terms at different times (below), and a round of an XCD's
+  // workgroups then holds as many of each, where row tiles taken whole fill a round with one kind.
+  int mt, nt;
+  if (vec & kLoraEarly) {
+    const int m_tiles = base_blocks / ksplit / n_tiles, full = (m_tiles & ~1) * n_tiles;
+    mt = t < full ? (t / (2 * n_tiles)) * 2 + (t & 1) : m_tiles - 1;
+    nt = t < full ? (t % (2 * n_tiles)) >> 1 : t - full;
+  } else {
+    mt = t / n_tiles;
+    nt = t - mt * n_tiles;
+  }
   const int64_t T = r.tokens;
   constexpr int kRows = 32 * MB;  // the tile's rows (LDS buffers hold 256; rows past kRows are loaded, never used)
   const int64_t p0 = (int64_t)mt * kRows;
@@ -195,14 +206,22 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // wait for the x rows of step i + 2. After x(i + 1) come w(i + 1) and x(i + 2).
   const int nk = w.k / kTK / ksplit;  // this block's K steps, from step ks * nk
   const int kbase = ks * nk * kTK;
+  // Decode-shaped passes (kLoraEarly, set by the host for short segments) alternate the LoRA term's place by row tile:
+  // odd row tiles add it before their K loop, so while some workgroups stream sB from memory others run their MFMA
+  // loops. The order depends on the row tile alone, and the gated and plain forms of a group cut the same row tiles,
+  // so an output's sum is formed in the same order in both. (Not in 224-row tiles: their scalar registers do not hold
+  // both phases' state.) Such a tile loads its first x rows after the term, whose sB slots are in their buffers.
+  const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
+  const bool early = MB != 7 && lora && (vec & kLoraEarly) && (mt & 1);
   WStage s0, s1;
   fetch_w(s0, kbase);
-  dma_x(g_x0, kbase);
-  dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
+  if (!early) {
+    dma_x(g_x0, kbase);
+    dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
+  }
   // The LoRA epilogue's bookkeeping, read while the first x rows load (scalar loads, which the vector-memory waits do
   // not count): the tile's first and last adapter segments, the first two segments' adapters and their live ranks of
   // the tile's first matrix.
-  const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
   const int jlo = lora ? matrix_of(L, GATED ? nt * 128 : n0) : 0;
   // (each pair packed in one 64-bit word, segment s_lo's in the low half: an array indexed by the segment would be
   // placed in scratch memory)
@@ -228,19 +247,50 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   }
   auto half_of = [](uint64_t pair, int i) __attribute__((always_inline)) { return (int)(uint32_t)(pair >> (32 * i)); };
   // LoRA second factor. The tile's rows of the first factor (sorted order, 64 ranks of a matrix at a time) are staged
-  // in LDS once; then for each adapter segment crossing the tile its sB rows for the wave's columns come straight from
-  // memory as MFMA operands one segment ahead of their products (deeper, the decode-pool groups were 2-7% slower: a
-  // round of tiles' sB streams already queue at the memory), and the products are added with the first
-  // factors of rows outside the segment, and ranks past the adapter's live rank, set to zero. A decode-shaped tile
+  // in LDS once; then for each adapter segment crossing the tile the wave stages its sB rows (its 32 columns x 64
+  // ranks: 32 rows of 128 bytes) in an LDS slot of its own, one segment ahead of their products, by loads that write
+  // LDS directly, each instruction reading 8 whole 128-byte rows (loaded as MFMA operands, lane = column, each
+  // instruction touches 32 rows in 32-byte pieces, and a workgroup streams at about half the rate); the products are
+  // added with the first factors of rows outside the segment, and ranks past the adapter's live rank, set to zero. A
+  // decode-shaped tile
   // crosses ~64 segments, so their bookkeeping is read into lane tables (lane i: segment c0 + i's adapter, live rank
   // and bounds, 64 segments at a time) and taken with readlane, with no memory latency per segment; the first two
   // segments' adapters and live ranks of the first matrix were read in the prologue, so a prefill tile (one or two
   // segments) starts its sB loads at once. st0 (and st1, the gated form's second buffer) are the LDS buffers the first
   // factors are staged in: after the K loop any of the ring; before it (`early`) the two the loop writes last (g_x3 is
   // the output tile's only; g_x2 is first written by the loop's first step, after a barrier).
-  auto lora_term = [&](uint16_t* st0, uint16_t* st1) __attribute__((always_inline)) {
+  // sl0, sl1: the two LDS buffers of the slots (the wave's at 32 x 64 elements from their starts).
+  auto lora_term = [&](uint16_t* st0, uint16_t* st1, uint16_t* sl0, uint16_t* sl1) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)mid, (short)0, (int)((int64_t)T * L.rank_cap * 2), 0x00020000);  // < 2^31: checked on the host
+    uint16_t* const slot0 = sl0 + wave * 32 * kTK;
+    uint16_t* const slot1 = sl1 + wave * 32 * kTK;
+    // A segment's sB rows into a slot: row i is column c0 + i of matrix j (rows past the matrix read its column 0 and
+    // are never used), ranks rc .. rc + 63 of the adapter's row stride sbs (chunks past the row re-read its last 8:
+    // past the live rank, masked when used). Instruction i fills rows 8 i + (lane >> 3); lane l writes slot l & 7 of
+    // its row, which holds the row's 16-byte chunk swz_slot(row, l & 7), as in the x rows.
+    auto stage_b = [&](uint16_t* slot, const uint16_t* blk, int sbs, int rc, int c0, int cj)
+        __attribute__((always_inline)) {
+      MLORA_WAIT_LGKM0();  // the wave's reads of the slot are done
+      const __amdgpu_buffer_rsrc_t bres =
+          __builtin_amdgcn_make_buffer_rsrc((void*)blk, (short)0, cj * sbs * 2, 0x00020000);  // the matrix's sB
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        const int col = c0 + row;
+        const int ccr = col >= 0 && col < cj ? col : 0;
+        const uint32_t off = (uint32_t)((ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8)) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i * 8 * kTK), 16, off, 0, 0, 0);
+      }
+    };
+    // the wave's operands of a staged segment (lane l: column l & 31, ranks 16 k16 + 8 (l >> 5) .. +7 of the chunk),
+    // once its slot's loads have landed (the next segment's 4 may be in flight)
+    auto read_b = [&](const uint16_t* slot, uint4 (&bv)[4]) __attribute__((always_inline)) {
+      MLORA_WAIT_VM(4);
+      const uint4* sv = reinterpret_cast<const uint4*>(slot);
+#pragma unroll
+      for (int k16 = 0; k16 < 4; ++k16) bv[k16] = sv[swz(lane & 31, 2 * k16 + (lane >> 5)) >> 3];
+    };
     // one pass over the segments: `stage` stages the first factors, then per chunk of 64 segments the lane tables
     // (ta, tb, te: adapter and bounds; tl: live rank of matrix j) and the segments' products, sB one ahead.
     // `ahead`: the prologue's read-ahead applies (the first chunk of matrix jlo); `rc` the rank chunk
@@ -266,31 +316,34 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             live = __builtin_amdgcn_readlane(tl, i);
           }
         };
-        uint4 q0[4], q1[4];
         int k0, k1;
-        auto load = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+        auto load = [&](int s, uint16_t* slot, int& rk) __attribute__((always_inline)) {
           int a, live;
           seg(s, a, live);
-          load_seg(a, live, bv);
+          load_seg(a, live, slot);
           rk = s <= cend ? min(live - rc, kRankChunk) : 0;
         };
-        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+        auto apply = [&](int s, const uint16_t* slot, int rk) __attribute__((always_inline)) {
+          uint4 bv[4];
+          read_b(slot, bv);
           if (rk <= 0) return;
           const int i = s - c0;
           // the bounds relative to the tile (tile rows and segment bounds are below 2^31)
           apply_seg(__builtin_amdgcn_readlane(tb, i) - (int)p0, __builtin_amdgcn_readlane(te, i) - (int)p0, bv, rk);
         };
-        load(c0, q0, k0);
+        load(c0, slot0, k0);
         if (c0 == s_lo) {
           MLORA_WAIT_VM(4);  // the staged first factors have landed (the sB loads may be in flight)
           lds_sync();
         }
+        // (no exit between the halves: a path leaving the loop with one buffer's loads unconsumed made the compiler
+        // wait for every load in flight at the top of each iteration, one segment's sB in flight at a time; past
+        // the chunk the loads re-read its last segment and rk is 0)
         for (int s = c0; s <= cend; s += 2) {
-          load(s + 1, q1, k1);
-          apply(s, q0, k0);
-          if (s + 1 > cend) break;
-          load(s + 2, q0, k0);
-          apply(s + 1, q1, k1);
+          load(s + 1, slot1, k1);
+          apply(s, slot0, k0);
+          load(s + 2, slot0, k0);
+          apply(s + 1, slot1, k1);
         }
       }
     };
@@ -317,25 +370,33 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                    16, off, 0, 0, 0);
         }
       }
-      // the lane's staged rows: row mb * 32 + (lane & 31) of the buffer holding its matrix's ranks, whose 16-byte
-      // chunk c sits in slot c ^ key; the matrix's ranks start at chunk o8 (16 k16 + 8 (lane >> 5) then in chunk
-      // o8 + 2 k16 + (lane >> 5) <= 7 for every k16 below the capacity)
-      const uint4* mrow = reinterpret_cast<const uint4*>(j == 1 && two ? st1 : st0) + (lane & 31) * 8;
+      // the lane's staged rows: row mb * 32 + (lane & 31) of the buffer holding its matrix's ranks (st1 for the up
+      // waves when 2c > 64, else st0), whose 16-byte chunk c sits in slot c ^ key; the matrix's ranks start at chunk
+      // o8 (16 k16 + 8 (lane >> 5) then in chunk o8 + 2 k16 + (lane >> 5) <= 7 for every k16 below the capacity).
+      // Both buffers are read and one value kept: a read through a pointer to either buffer is not known to miss the
+      // sB slots, and the compiler would wait for every slot load in flight before each such read.
+      const bool in1 = j == 1 && two;
+      const uint4* mrow0 = reinterpret_cast<const uint4*>(st0) + (lane & 31) * 8;
+      const uint4* mrow1 = reinterpret_cast<const uint4*>(st1) + (lane & 31) * 8;
       const int key = ((lane & 31) >> 1) & 7;
       const int cb = (j == 1 && !two ? capj / 8 : 0) + (lane >> 5);
-      const int ccol = wcol - (j ? inter : 0);        // the lane's column inside its matrix
+      const int wcj = wc0 - (j ? inter : 0);  // the wave's first column inside its matrix
       __builtin_amdgcn_sched_barrier(0);  // the staging loads are issued before every load below
+      // the first factors of row block cmb (its rows 32 cmb + (lane & 31), 64 ranks of the wave's matrix), read from
+      // LDS when a segment first touches the block and kept for the next segments (a decode-shaped block holds ~8)
+      uint4 av[4];
+      int cmb = -1;
       // per chunk of 64 segments, lane tables (lane i: segment c0 + i's adapter, bounds relative to the tile, and
-      // live rank of the wave's matrix), then each segment's sB operands one segment ahead of its products
+      // live rank of the wave's matrix), then each segment's sB rows one segment ahead of its products
       for (int c0 = s_lo; c0 <= s_hi; c0 += kWave) {
         const int cend = min(c0 + kWave - 1, s_hi);  // the chunk's last segment
         const int sc = min(c0 + lane, cend);
         const int ta = r.seg_adapter[sc];
         const int tb = r.seg_start[sc] - (int)p0, te = r.seg_start[sc + 1] - (int)p0;  // tile rows: below 2^31
         const int tl = ta == 0 ? 0 : live_rank(L, ta, j);
-        // sB operands of segment s for ranks 16 k16 + 8 (lane >> 5) .. +7, zero past live rank `rk` (0 past the
-        // chunk: the loads then re-read its last segment's)
-        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+        // segment s's sB rows into a slot, and its live rank `rk` (0 past the chunk: the loads then re-read its last
+        // segment's)
+        auto load_b = [&](int s, uint16_t* slot, int& rk) __attribute__((always_inline)) {
           const int i = min(s, cend) - c0;
           int a, live;
           if (c0 == s_lo && i < 2) {  // read ahead in the prologue
@@ -346,46 +407,50 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             live = __builtin_amdgcn_readlane(tl, i);
           }
           rk = s <= cend ? live : 0;
-          const int sbs = sb_stride(live, capj);
-          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
-#pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            const int q = min(16 * k16 + 8 * (lane >> 5), sbs - 8);
-            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
-          }
+          stage_b(slot, L.pool + (int64_t)a * L.pool_stride + L.off_b[j], sb_stride(live, capj), 0, wcj, inter);
         };
-        auto apply = [&](int s, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+        // its products, the operands read from the slot, zero past live rank `rk`
+        auto apply = [&](int s, const uint16_t* slot, int rk) __attribute__((always_inline)) {
+          uint4 bv[4];
+          read_b(slot, bv);
           if (rk <= 0) return;
           const int sb = __builtin_amdgcn_readlane(tb, s - c0), se = __builtin_amdgcn_readlane(te, s - c0);
+          // ranks past the live rank: zero in both operands (the first factors there are not written: masked only
+          // when the live rank is below the chunk)
 #pragma unroll
           for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
             if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
-            const int row = mb * 32 + (lane & 31);
-            const bool rin = row >= sb && row < se;
+            if (cmb != mb) {
+#pragma unroll
+              for (int k16 = 0; k16 < 4; ++k16) {
+                const uint4 a0 = mrow0[mb * 256 + ((cb + 2 * k16) ^ key)];
+                const uint4 a1 = mrow1[mb * 256 + ((cb + 2 * k16) ^ key)];
+                av[k16] = in1 ? a1 : a0;
+              }
+              cmb = mb;
+            }
+            const bool rin = mb * 32 + (lane & 31) >= sb && mb * 32 + (lane & 31) < se;
 #pragma unroll
             for (int k16 = 0; k16 < 4; ++k16) {
-              if (16 * k16 >= rk) break;
-              uint4 av = mrow[mb * 256 + ((cb + 2 * k16) ^ key)];
-              av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-              acc[mb] = mfma32(bv[k16], av, acc[mb]);
+              uint4 v = rin ? av[k16] : make_uint4(0, 0, 0, 0);
+              if (rk < kRankChunk) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
+              acc[mb] = mfma32(bv[k16], v, acc[mb]);
             }
           }
         };
-        uint4 b0[4], b1[4];
         int rk0, rk1;
-        load_b(c0, b0, rk0);
+        load_b(c0, slot0, rk0);
         if (c0 == s_lo) {
           MLORA_WAIT_VM(4);  // the first factors have landed (the 4 sB loads may still be in flight)
           lds_sync();
         }
-        for (int s = c0; s <= cend; s += 2) {
-          load_b(s + 1, b1, rk1);
-          apply(s, b0, rk0);
-          if (s + 1 > cend) break;
-          load_b(s + 2, b0, rk0);
-          apply(s + 1, b1, rk1);
+        for (int s = c0; s <= cend; s += 2) {  // (no exit between the halves, as in the plain form)
+          load_b(s + 1, slot1, rk1);
+          apply(s, slot0, rk0);
+          load_b(s + 2, slot0, rk0);
+          apply(s + 1, slot1, rk1);
         }
       }
     } else {
@@ -395,8 +460,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         // the wave's column inside matrix j (others get zero operands)
         const int cc = wc0 + (lane & 31);
         const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
-        const int ccol = (cin ? cc : oj) - oj;
         for (int rc = 0; rc < capj; rc += kRankChunk) {
+          // the first factors of row block cmb, read from LDS when a segment first touches the block and kept for the
+          // next segments (a decode-shaped block holds ~8)
+          uint4 av[4];
+          int cmb = -1;
           pass(j, rc, j == jlo,
                // first factors of the tile's rows: 256 rows x 64 ranks, rows of 128 bytes swizzled like x
                [&]() __attribute__((always_inline)) {
@@ -410,15 +478,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                                                             off, 0, 0, 0);
                  }
                },
-               // sB operands for ranks rc + 16 k16 + 8 (lane >> 5) .. +7 (clamped to the adapter's block)
-               [&](int a, int live, uint4 (&bv)[4]) __attribute__((always_inline)) {
-                 const int sbs = sb_stride(live, capj);  // the adapter's sB row stride (at least 8: capj > rc >= 0)
-                 const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
-#pragma unroll
-                 for (int k16 = 0; k16 < 4; ++k16) {
-                   const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
-                   bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
-                 }
+               // the segment's sB rows for ranks rc .. rc + 63 into a slot (the adapter's row stride sbs is at least 8:
+               // capj > rc >= 0)
+               [&](int a, int live, uint16_t* slot) __attribute__((always_inline)) {
+                 stage_b(slot, L.pool + (int64_t)a * L.pool_stride + L.off_b[j], sb_stride(live, capj), rc, wc0 - oj,
+                         cj);
                },
                [&](int sb, int se, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
                  // (sb, se: the segment's bounds relative to the tile's first row)
@@ -429,28 +493,33 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                  for (int mb = 0; mb < MB; ++mb) {
                    if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
                    const int row = mb * 32 + (lane & 31);
+                   if (cmb != mb) {
+#pragma unroll
+                     for (int k16 = 0; k16 < 4; ++k16)
+                       av[k16] = reinterpret_cast<const uint4*>(st0)[swz(row, 2 * k16 + (lane >> 5)) >> 3];
+                     cmb = mb;
+                   }
                    const bool rin = row >= sb && row < se;
+                   // (ranks past the live rank are zero in both operands: the first factors there are not written)
 #pragma unroll
                    for (int k16 = 0; k16 < 4; ++k16) {
-                     if (16 * k16 >= rk) break;
-                     uint4 av =
-                         reinterpret_cast<const uint4*>(st0)[swz(mb * 32 + (lane & 31), 2 * k16 + (lane >> 5)) >> 3];
-                     av = rin ? keep_first(av, rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
-                     acc[mb] = mfma32(bv[k16], av, acc[mb]);
+                     uint4 v = rin ? av[k16] : make_uint4(0, 0, 0, 0);
+                     if (rk < kRankChunk) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
+                     acc[mb] = mfma32(bv[k16], v, acc[mb]);
                    }
                  }
                });
         }
       }
     }
+    MLORA_WAIT_VM(0);  // the last slot loads (past the last segment) have landed before their buffers are reused
   };
-  // Decode-shaped passes (kLoraEarly, set by the host for short segments) alternate the term's place by row tile: odd
-  // row tiles add it before their K loop, so while some workgroups stream sB from memory others run their MFMA loops
-  // (all at once, the sB streams of a round of tiles queue at the memory). The order depends on the row tile alone,
-  // and the gated and plain forms of a group cut the same row tiles, so an output's sum is formed in the same order
-  // in both. (Not in 224-row tiles: their scalar registers do not hold both phases' state.)
-  const bool early = MB != 7 && lora && (vec & kLoraEarly) && (mt & 1);
-  if (early) lora_term(g_x3, g_x2);
+  if (early) {
+    lora_term(g_x3, g_x2, g_x0, g_x1);
+    lds_sync();  // every wave is done with its sB slots
+    dma_x(g_x0, kbase);
+    dma_x(g_x1, kbase + min(1, nk - 1) * kTK);
+  }
   MLORA_WAIT_VM(kXLoads);  // x(0) has landed
   step_sync();
   load_a(g_x0, 0, a);
@@ -503,7 +572,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
     return;
   }
 
-  if (lora && !early) lora_term(g_x0, g_x1);
+  if (lora && !early) lora_term(g_x0, g_x1, g_x2, g_x3);
 
   // Single rounding to bf16 and the stores, through LDS (the whole tile at once): lane l holds, for row
   // mb * 32 + (l & 31), the four consecutive columns 8 g + 4 (l >> 5) .. +3 of its wave's 32 columns; every wave

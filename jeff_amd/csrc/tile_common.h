@@ -22,6 +22,8 @@ __device__ __forceinline__ int swz(int row, int c) { return row * kTK + (swz_slo
 // Wait until at most n vector memory instructions of this wave are outstanding and its LDS operations are done
 // (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0).
 #define MLORA_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+// ... and until its LDS operations are done, vector memory instructions left in flight (vmcnt at its maximum, 63)
+#define MLORA_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4))
 
 // Workgroup barrier that orders LDS accesses only (global stores in flight are not waited for).
 __device__ __forceinline__ void lds_sync() {
