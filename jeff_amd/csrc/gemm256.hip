@@ -417,8 +417,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
           const int sb = __builtin_amdgcn_readlane(tb, s - c0), se = __builtin_amdgcn_readlane(te, s - c0);
           // ranks past the live rank: zero in both operands (the first factors there are not written: masked only
           // when the live rank is below the chunk)
+          const bool partial = rk < kRankChunk;  // (one wave-uniform branch around each group of masks)
+          if (partial) {
 #pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+            for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+          }
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
             if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
@@ -432,12 +435,15 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
               cmb = mb;
             }
             const bool rin = mb * 32 + (lane & 31) >= sb && mb * 32 + (lane & 31) < se;
+            uint4 v[4];
 #pragma unroll
-            for (int k16 = 0; k16 < 4; ++k16) {
-              uint4 v = rin ? av[k16] : make_uint4(0, 0, 0, 0);
-              if (rk < kRankChunk) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
-              acc[mb] = mfma32(bv[k16], v, acc[mb]);
+            for (int k16 = 0; k16 < 4; ++k16) v[k16] = rin ? av[k16] : make_uint4(0, 0, 0, 0);
+            if (partial) {
+#pragma unroll
+              for (int k16 = 0; k16 < 4; ++k16) v[k16] = keep_first(v[k16], rk - (16 * k16 + 8 * (lane >> 5)));
             }
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) acc[mb] = mfma32(bv[k16], v[k16], acc[mb]);
           }
         };
         int rk0, rk1;
@@ -486,9 +492,13 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                },
                [&](int sb, int se, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
                  // (sb, se: the segment's bounds relative to the tile's first row)
+                 const bool partial = rk < kRankChunk;  // (one wave-uniform branch around each group of masks)
 #pragma unroll
-                 for (int k16 = 0; k16 < 4; ++k16)
-                   bv[k16] = cin ? keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5))) : make_uint4(0, 0, 0, 0);
+                 for (int k16 = 0; k16 < 4; ++k16) bv[k16] = cin ? bv[k16] : make_uint4(0, 0, 0, 0);
+                 if (partial) {
+#pragma unroll
+                   for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+                 }
 #pragma unroll
                  for (int mb = 0; mb < MB; ++mb) {
                    if (mb * 32 >= se || mb * 32 + 32 <= sb) continue;
@@ -504,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 #pragma unroll
                    for (int k16 = 0; k16 < 4; ++k16) {
                      uint4 v = rin ? av[k16] : make_uint4(0, 0, 0, 0);
-                     if (rk < kRankChunk) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
+                     if (partial) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
                      acc[mb] = mfma32(bv[k16], v, acc[mb]);
                    }
                  }
