@@ -415,10 +415,11 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
           read_b(slot, bv);
           if (rk <= 0) return;
           const int sb = __builtin_amdgcn_readlane(tb, s - c0), se = __builtin_amdgcn_readlane(te, s - c0);
-          // ranks past the live rank: zero in both operands (the first factors there are not written: masked only
-          // when the live rank is below the chunk)
-          const bool partial = rk < kRankChunk;  // (one wave-uniform branch around each group of masks)
-          if (partial) {
+          // products of the 16-rank groups below the live rank; when the live rank is not a multiple of 16, the
+          // ranks past it in its last group are zeroed in both operands (the first factors there are not written)
+          const int nk = (rk + 15) >> 4;
+          const bool ragged = (rk & 15) != 0;
+          if (ragged) {
 #pragma unroll
             for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
           }
@@ -428,8 +429,8 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             if (cmb != mb) {
 #pragma unroll
               for (int k16 = 0; k16 < 4; ++k16) {
-                const uint4 a0 = mrow0[mb * 256 + ((cb + 2 * k16) ^ key)];
-                const uint4 a1 = mrow1[mb * 256 + ((cb + 2 * k16) ^ key)];
+                const uint4 a0 = mrow0[mb * 256 + (((cb + 2 * k16) & 7) ^ key)];
+                const uint4 a1 = mrow1[mb * 256 + (((cb + 2 * k16) & 7) ^ key)];
                 av[k16] = in1 ? a1 : a0;
               }
               cmb = mb;
@@ -438,12 +439,13 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
             uint4 v[4];
 #pragma unroll
             for (int k16 = 0; k16 < 4; ++k16) v[k16] = rin ? av[k16] : make_uint4(0, 0, 0, 0);
-            if (partial) {
+            if (ragged) {
 #pragma unroll
               for (int k16 = 0; k16 < 4; ++k16) v[k16] = keep_first(v[k16], rk - (16 * k16 + 8 * (lane >> 5)));
             }
 #pragma unroll
-            for (int k16 = 0; k16 < 4; ++k16) acc[mb] = mfma32(bv[k16], v[k16], acc[mb]);
+            for (int k16 = 0; k16 < 4; ++k16)
+              if (k16 < nk) acc[mb] = mfma32(bv[k16], v[k16], acc[mb]);
           }
         };
         int rk0, rk1;
@@ -491,13 +493,16 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                          cj);
                },
                [&](int sb, int se, uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
-                 // (sb, se: the segment's bounds relative to the tile's first row)
-                 const bool partial = rk < kRankChunk;  // (one wave-uniform branch around each group of masks)
+                 // (sb, se: the segment's bounds relative to the tile's first row; products of the 16-rank groups
+                 // below the live rank, the ranks past it in a part-live last group zeroed in both operands)
+                 const int nk = (rk + 15) >> 4;
+                 const bool ragged = (rk & 15) != 0;
 #pragma unroll
                  for (int k16 = 0; k16 < 4; ++k16) bv[k16] = cin ? bv[k16] : make_uint4(0, 0, 0, 0);
-                 if (partial) {
+                 if (ragged) {
 #pragma unroll
-                   for (int k16 = 0; k16 < 4; ++k16) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
+                   for (int k16 = 0; k16 < 4; ++k16)
+                     if (k16 == nk - 1) bv[k16] = keep_first(bv[k16], rk - (16 * k16 + 8 * (lane >> 5)));
                  }
 #pragma unroll
                  for (int mb = 0; mb < MB; ++mb) {
@@ -505,16 +510,18 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
                    const int row = mb * 32 + (lane & 31);
                    if (cmb != mb) {
 #pragma unroll
-                     for (int k16 = 0; k16 < 4; ++k16)
+                     for (int k16 = 0; k16 < 4; ++k16) {
+                       if (16 * k16 >= capj - rc) break;  // (groups past the capacity are never used)
                        av[k16] = reinterpret_cast<const uint4*>(st0)[swz(row, 2 * k16 + (lane >> 5)) >> 3];
+                     }
                      cmb = mb;
                    }
                    const bool rin = row >= sb && row < se;
-                   // (ranks past the live rank are zero in both operands: the first factors there are not written)
 #pragma unroll
                    for (int k16 = 0; k16 < 4; ++k16) {
+                     if (k16 >= nk) break;
                      uint4 v = rin ? av[k16] : make_uint4(0, 0, 0, 0);
-                     if (partial) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
+                     if (ragged && k16 == nk - 1) v = keep_first(v, rk - (16 * k16 + 8 * (lane >> 5)));
                      acc[mb] = mfma32(bv[k16], v, acc[mb]);
                    }
                  }
