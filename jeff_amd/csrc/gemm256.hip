@@ -48,8 +48,10 @@ __shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it
 
 // MB: 32-row blocks of a tile (8: 256 rows; 7: 224 and 4: 128 rows, chosen by the host when they take fewer rounds
 // of tiles);
-// GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none of it
-template <int MB, bool GATED>
+// GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none of it;
+// EARLY: the kernel may add the LoRA term before the K loop (decode-shaped passes, below). The prefill kernels carry
+// no such path: with it, the compiler waits for every load in flight at the top of each round of the K loop.
+template <int MB, bool GATED, bool EARLY>
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
                                                                uint16_t* __restrict__ y, int64_t y_stride,
@@ -209,10 +211,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   // Decode-shaped passes (kLoraEarly, set by the host for short segments) alternate the LoRA term's place by row tile:
   // odd row tiles add it before their K loop, so while some workgroups stream sB from memory others run their MFMA
   // loops. The order depends on the row tile alone, and the gated and plain forms of a group cut the same row tiles,
-  // so an output's sum is formed in the same order in both. (Not in 224-row tiles: their scalar registers do not hold
-  // both phases' state.) Such a tile loads its first x rows after the term, whose sB slots are in their buffers.
+  // so an output's sum is formed in the same order in both. Such a tile loads its first x rows after the term, whose
+  // sB slots are in their buffers.
   const bool lora = part == nullptr && L.n_mats > 0 && mid != nullptr;
-  const bool early = MB != 7 && lora && (vec & kLoraEarly) && (mt & 1);
+  const bool early = EARLY && lora && (vec & kLoraEarly) && (mt & 1);
   WStage s0, s1;
   fetch_w(s0, kbase);
   if (!early) {
@@ -554,18 +556,29 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
-  for (int it = 0; it < nk; it += 6) {
+  // Whole rounds of six steps in a loop with no other exit (an exit inside the loop made the compiler wait for every
+  // load in flight at the top of each round, the x rows two steps ahead included), then the remaining steps.
+  const int nfull = nk - nk % 6;
+  for (int it = 0; it < nfull; it += 6) {
     run(I0{}, I0{}, it);
-    if (it + 1 >= nk) break;
     run(I1{}, I1{}, it + 1);
-    if (it + 2 >= nk) break;
     run(I2{}, I0{}, it + 2);
-    if (it + 3 >= nk) break;
     run(I0{}, I1{}, it + 3);
-    if (it + 4 >= nk) break;
     run(I1{}, I0{}, it + 4);
-    if (it + 5 >= nk) break;
     run(I2{}, I1{}, it + 5);
+  }
+  if (nfull < nk) {
+    run(I0{}, I0{}, nfull);
+    if (nfull + 1 < nk) {
+      run(I1{}, I1{}, nfull + 1);
+      if (nfull + 2 < nk) {
+        run(I2{}, I0{}, nfull + 2);
+        if (nfull + 3 < nk) {
+          run(I0{}, I1{}, nfull + 3);
+          if (nfull + 4 < nk) run(I1{}, I0{}, nfull + 4);
+        }
+      }
+    }
   }
   MLORA_WAIT_VM(0);
   lds_sync();
@@ -714,10 +727,15 @@ int launch_base256(const mlora_int4_t& w, const mlora_lora_t& L, const mlora_rou
                    (last_out == nullptr || reinterpret_cast<uintptr_t>(last_out) % 16 == 0);  // gated: inter % 128 == 0
   const bool early = part == nullptr && r.tokens < 16 * (segs > 0 ? segs : 1);  // decode-shaped: alternate the order
   const dim3 grid((unsigned)blocks);
-  auto kernel = inter > 0 ? (mb == 4 ? base_mfma256_kernel<4, true>
-                                     : mb == 7 ? base_mfma256_kernel<7, true> : base_mfma256_kernel<8, true>)
-                          : (mb == 4 ? base_mfma256_kernel<4, false>
-                                     : mb == 7 ? base_mfma256_kernel<7, false> : base_mfma256_kernel<8, false>);
+  // (224-row tiles have no early form: their scalar registers do not hold both phases' state)
+  auto kernel = inter > 0 ? (mb == 4   ? base_mfma256_kernel<4, true, true>
+                             : mb == 7 ? base_mfma256_kernel<7, true, false>
+                             : early   ? base_mfma256_kernel<8, true, true>
+                                       : base_mfma256_kernel<8, true, false>)
+                          : (mb == 4   ? base_mfma256_kernel<4, false, true>
+                             : mb == 7 ? base_mfma256_kernel<7, false, false>
+                             : early   ? base_mfma256_kernel<8, false, true>
+                                       : base_mfma256_kernel<8, false, false>);
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, w, L, r, x, x_stride, y, y_stride, last_out, n_out, mid,
                      n_tiles, (vec ? kStoreVec : 0) | (residual ? kStoreResidual : 0) | (early ? kLoraEarly : 0), part,
                      ksplit, (int32_t)blocks,
