@@ -11,8 +11,9 @@
 // One input range (the columns alone fill the CUs): the first factors are computed first (shrink_seg.h, their own
 // launch), and the tile adds the LoRA term after its K loop: the first factors of the wave's rows (64 ranks of matrix
 // j) are loaded before the loop; the adapter segments crossing those rows are listed one per lane (adapter, live
-// rank), and their sB operands stream from memory four segments ahead of the MFMAs. A segment's term goes into the
-// row blocks it crosses, with the first factors of rows outside the segment, and ranks past its live rank, set to
+// rank), and each segment's sB rows (the wave's 32 columns) are staged in an LDS slot of the wave's own (the x ring
+// is idle by then) by loads that write LDS directly, whole 128-byte rows, one segment ahead of its MFMAs (the expand
+// launch below stages them the same way). A segment's term goes into the row blocks it crosses, with the first factors of rows outside the segment, and ranks past its live rank, set to
 // zero. The tile is rounded once and written (plain, added to the residual, or silu(gate) * up).
 // S input ranges (the columns alone are too few for the CUs): two launches, neither waiting for another workgroup.
 // The first is the ranges' base tiles, each writing its float32 tile in the accumulators' own order (one coalesced
@@ -302,6 +303,9 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   };
   for (int it = 0; it < nk; it += 12) steps_from<0>(run, it, nk);
   MLORA_WAIT_VM(0);
+  // (the LoRA term stages sB in the ring's last two buffers: every wave's reads of the ring and x loads into it are
+  // done first)
+  if (!RANGES && L.n_mats > 0 && mid != nullptr) lds_sync();
 
   if constexpr (RANGES) {
     // this range's float32 tile, in the accumulators' order
@@ -322,7 +326,6 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j];
       const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
       const bool allin = cw0 >= oj && cw0 + 32 <= oj + cj && cw0 + 32 <= n_out;  // every lane's column in matrix j
-      const int ccol = (cin ? cc : oj) - oj;
       const int llive = j == jlo ? llive0 : (la == 0 ? 0 : live_rank(L, la, j));
       for (int rc = 0; rc < capj; rc += kDRankChunk) {
         uint4 m[kDMB][4];
@@ -334,11 +337,14 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
         } else {
           load_mid(m, j, rc);
         }
-        // sB operands of segment s (ranks rc + 16 k16 + 8 (lane >> 5) .. +7): unconditional loads inside the
-        // adapter's block (clamped to its last 8 ranks), masked when used
-        // The wave's first 64 segments are held one per lane; empty segments (requests of no tokens) can put more
-        // than 64 segment indices across its 64 rows, and those past the 64th are read from memory (i is uniform).
-        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+        // Segment s's sB rows into an LDS slot of the wave's own (4 KB: its 32 columns x ranks rc .. rc + 63, rows
+        // of 128 bytes swizzled like x), by loads that write LDS directly, one segment ahead of the segment's
+        // products: instruction i fills rows 8 i + (lane >> 3) (row = the wave's column, clamped into matrix j;
+        // chunks past the adapter's row re-read its last 8 ranks, masked when used), so each instruction reads 8
+        // whole rows. The wave's first 64 segments are held one per lane; empty segments (requests of no tokens) can
+        // put more than 64 segment indices across its 64 rows, and those past the 64th are read from memory (i is
+        // uniform).
+        auto load_b = [&](int s, uint16_t* slot, int& rk) __attribute__((always_inline)) {
           const int sc = min(s, s_hi), i = sc - s_lo;
           int a, live;
           if (i < kWave) {
@@ -350,15 +356,29 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
           }
           rk = s <= s_hi ? min(live - rc, kDRankChunk) : 0;
           const int sbs = sb_stride(live, capj);  // at least 8: capj > rc >= 0
-          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+          MLORA_WAIT_LGKM0();                     // the wave's reads of the slot are done
+          const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+              (void*)(L.pool + (int64_t)a * L.pool_stride + L.off_b[j]), (short)0, cj * sbs * 2, 0x00020000);
 #pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
-            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const int row = 8 * i4 + (lane >> 3);
+            const int col = cw0 - oj + row;
+            const int ccr = col >= 0 && col < cj ? col : 0;
+            const uint32_t off = (uint32_t)((ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8)) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i4 * 8 * kTK), 16, off, 0, 0, 0);
           }
         };
         {
-          auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+          uint16_t* const slot0 = d_x2 + wave * 32 * kTK;
+          uint16_t* const slot1 = d_x3 + wave * 32 * kTK;
+          // the slot's operands (lane l: column l & 31, ranks 16 k16 + 8 (l >> 5) .. +7 of the chunk) once its loads
+          // have landed (the next segment's 4 may be in flight), then the segment's products
+          auto apply = [&](int s, const uint16_t* slot, int rk) __attribute__((always_inline)) {
+            MLORA_WAIT_VM(4);
+            uint4 bv[4];
+            const uint4* sv = reinterpret_cast<const uint4*>(slot);
+#pragma unroll
+            for (int k16 = 0; k16 < 4; ++k16) bv[k16] = sv[swz(lane & 31, 2 * k16 + (lane >> 5)) >> 3];
             if (rk <= 0) return;
             uint32_t rmask[kDMB];
 #pragma unroll
@@ -378,13 +398,9 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
               }
             }
           };
-          uint4 q0[4], q1[4], q2[4], q3[4];
-          int k0, k1, k2, k3;
-          load_b(s_lo, q0, k0);
-          load_b(s_lo + 1, q1, k1);
-          load_b(s_lo + 2, q2, k2);
-          load_b(s_lo + 3, q3, k3);
-          // Each row's first factors past its own segment's live rank are set to zero once, while the first segments'
+          int k0, k1;
+          load_b(s_lo, slot0, k0);
+          // Each row's first factors past its own segment's live rank are set to zero once, while the first segment's
           // sB loads are in flight (the segment's live rank from its lane of llive, or from memory past the wave's
           // first 64 segments; rows past the pass have none): a segment's term then needs only a row mask on the first
           // factors, and the sB chunk crossing the live rank (rk not a multiple of 16) keeps only its live ranks, so
@@ -402,16 +418,14 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             for (int k16 = 0; k16 < 4; ++k16)
               m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
           }
-          for (int s = s_lo; s <= s_hi; s += 4) {
-            apply(s, q0, k0);
-            load_b(s + 4, q0, k0);
-            apply(s + 1, q1, k1);
-            load_b(s + 5, q1, k1);
-            apply(s + 2, q2, k2);
-            load_b(s + 6, q2, k2);
-            apply(s + 3, q3, k3);
-            load_b(s + 7, q3, k3);
+          // (no exit between the halves: past s_hi the loads re-read its last segment and rk is 0)
+          for (int s = s_lo; s <= s_hi; s += 2) {
+            load_b(s + 1, slot1, k1);
+            apply(s, slot0, k0);
+            load_b(s + 2, slot0, k0);
+            apply(s + 1, slot1, k1);
           }
+          MLORA_WAIT_VM(0);  // the last slot loads have landed before the slots are staged again or reused
         }
       }
     }
@@ -597,7 +611,6 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
       const int oj = col_offset(L, j), cj = L.cols[j], capj = L.cap[j];
       const bool cin = cc >= oj && cc < oj + cj && cc < n_out;
       const bool allin = cw0 >= oj && cw0 + 32 <= oj + cj && cw0 + 32 <= n_out;  // every lane's column in matrix j
-      const int ccol = (cin ? cc : oj) - oj;
       const int llive = j == jlo ? llive0 : (la == 0 ? 0 : live_rank(L, la, j));
       for (int rc = 0; rc < capj; rc += kDRankChunk) {
         uint4 m[kDMB][4];
@@ -609,11 +622,13 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
         } else {
           load_mid(m, j, rc);
         }
-        // sB operands of segment s (ranks rc + 16 k16 + 8 (lane >> 5) .. +7): unconditional loads inside the
-        // adapter's block (clamped to its last 8 ranks), masked when used
-        // The wave's first 64 segments are held one per lane; empty segments (requests of no tokens) can put more
-        // than 64 segment indices across its 64 rows, and those past the 64th are read from memory (i is uniform).
-        auto load_b = [&](int s, uint4 (&bv)[4], int& rk) __attribute__((always_inline)) {
+        // Segment s's sB rows into an LDS slot of the wave's own (its 32 columns x ranks rc .. rc + 63, rows of 128
+        // bytes swizzled like x) by loads that write LDS directly, each instruction 8 whole rows (row = the wave's
+        // column, clamped into matrix j; chunks past the adapter's row re-read its last 8 ranks, masked when used),
+        // one of the wave's segments ahead of its products. The wave's first 64 segments are held one per lane; empty
+        // segments (requests of no tokens) can put more than 64 segment indices across its 64 rows, and those past
+        // the 64th are read from memory (i is uniform).
+        auto load_b = [&](int s, uint16_t* slot, int& rk) __attribute__((always_inline)) {
           const int sc = min(s, s_hi), i = sc - s_lo;
           int a, live;
           if (i < kWave) {
@@ -625,14 +640,35 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
           }
           rk = s <= s_hi ? min(live - rc, kDRankChunk) : 0;
           const int sbs = sb_stride(live, capj);  // at least 8: capj > rc >= 0
-          const uint16_t* brow = L.pool + (int64_t)a * L.pool_stride + L.off_b[j] + (int64_t)ccol * sbs;
+          MLORA_WAIT_LGKM0();                     // the wave's reads of the slot are done
+          const uint16_t* blk = L.pool + (int64_t)a * L.pool_stride + L.off_b[j];
+          // (through a buffer resource; the gated form, whose scalar registers are fewer to spare, by 64-bit
+          // addresses: with the resource it reserved a scratch frame)
+          const __amdgpu_buffer_rsrc_t bres =
+              __builtin_amdgcn_make_buffer_rsrc((void*)blk, (short)0, GATED ? 0 : cj * sbs * 2, 0x00020000);
 #pragma unroll
-          for (int k16 = 0; k16 < 4; ++k16) {
-            const int q = min(rc + 16 * k16 + 8 * (lane >> 5), sbs - 8);
-            bv[k16] = *reinterpret_cast<const uint4*>(brow + q);
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const int row = 8 * i4 + (lane >> 3);
+            const int col = cw0 - oj + row;
+            const int ccr = col >= 0 && col < cj ? col : 0;
+            const int q = ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8);
+            if constexpr (GATED)
+              __builtin_amdgcn_global_load_lds((const void*)(blk + q), (lds_void*)(slot + i4 * 8 * kTK), 16, 0, 0);
+            else
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i4 * 8 * kTK), 16, (uint32_t)q * 2, 0,
+                                                       0, 0);
           }
         };
-        auto apply = [&](int s, const uint4 (&bv)[4], int rk) __attribute__((always_inline)) {
+        uint16_t* const slot0 = d_x2 + ew * 32 * kTK;  // (the base launch's x buffers: 4 KB a wave in each)
+        uint16_t* const slot1 = d_x3 + ew * 32 * kTK;
+        // the slot's operands (lane l: column l & 31, ranks 16 k16 + 8 (l >> 5) .. +7 of the chunk) once its loads
+        // have landed (the next segment's 4 may be in flight), then the segment's products
+        auto apply = [&](int s, const uint16_t* slot, int rk) __attribute__((always_inline)) {
+          MLORA_WAIT_VM(4);
+          uint4 bv[4];
+          const uint4* sv = reinterpret_cast<const uint4*>(slot);
+#pragma unroll
+          for (int k16 = 0; k16 < 4; ++k16) bv[k16] = sv[swz(lane & 31, 2 * k16 + (lane >> 5)) >> 3];
           if (rk <= 0) return;
           uint32_t rmask[kDMB];
 #pragma unroll
@@ -652,11 +688,9 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
             }
           }
         };
-        uint4 q0[4], q1[4];
         int k0, k1;
-        load_b(s_lo + sg, q0, k0);
-        load_b(s_lo + sg + kESG, q1, k1);
-        // Each row's first factors past its own segment's live rank are set to zero once, while the first segments'
+        load_b(s_lo + sg, slot0, k0);
+        // Each row's first factors past its own segment's live rank are set to zero once, while the first segment's
         // sB loads are in flight (the segment's live rank from its lane of llive, or from memory past the wave's
         // first 64 segments; rows past the pass have none): a segment's term then needs only a row mask on the first
         // factors, and the sB chunk crossing the live rank (rk not a multiple of 16) keeps only its live ranks, so
@@ -674,12 +708,14 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
           for (int k16 = 0; k16 < 4; ++k16)
             m[mb][k16] = keep_first(m[mb][k16], rrow - rc - (16 * k16 + 8 * (lane >> 5)));
         }
+        // (no exit between the halves: past s_hi the loads re-read its last segment and rk is 0)
         for (int s = s_lo + sg; s <= s_hi; s += 2 * kESG) {
-          apply(s, q0, k0);
-          load_b(s + 2 * kESG, q0, k0);
-          apply(s + kESG, q1, k1);
-          load_b(s + 3 * kESG, q1, k1);
+          load_b(s + kESG, slot1, k1);
+          apply(s, slot0, k0);
+          load_b(s + 2 * kESG, slot0, k0);
+          apply(s + kESG, slot1, k1);
         }
+        MLORA_WAIT_VM(0);  // the last slot loads have landed before the slots are staged again
       }
     }
   }
