@@ -559,6 +559,20 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
     lq[mb] = sg == 0 && row < T && last_out != nullptr ? r.last_of[row] : -1;
   }
 
+  // (the segments' adapters are asked for before the ranges' tiles are added, so their loads run beside that sum)
+  if (lora) {
+#pragma unroll
+    for (int mb = 0; mb < kDMB; ++mb) {
+      const int last = r_end - 1 - (R0 + mb * 32);  // the block's last row in the pass, relative to its first
+      blo[mb] = last >= 0 ? __builtin_amdgcn_readfirstlane(rseg[mb]) : INT_MAX;
+      bhi[mb] = last >= 0 ? __builtin_amdgcn_readlane(rseg[mb], min(last, 31)) : -1;
+    }
+    s_lo = blo[0];
+    s_hi = bhi[kDMB - 1] >= 0 ? bhi[kDMB - 1] : bhi[0];
+    la = s_lo + lane <= s_hi ? r.seg_adapter[s_lo + lane] : 0;
+    llive0 = la == 0 ? 0 : live_rank(L, la, jlo);
+  }
+
   // segment group 0: the ranges' tiles added in order, four ranges' loads in flight at a time
   f32x16_t acc[kDMB];
 #pragma unroll
@@ -588,19 +602,6 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
             acc[mb][4 * g + 3] += u[i][e].w;
           }
         }
-  }
-
-  if (lora) {
-#pragma unroll
-    for (int mb = 0; mb < kDMB; ++mb) {
-      const int last = r_end - 1 - (R0 + mb * 32);  // the block's last row in the pass, relative to its first
-      blo[mb] = last >= 0 ? __builtin_amdgcn_readfirstlane(rseg[mb]) : INT_MAX;
-      bhi[mb] = last >= 0 ? __builtin_amdgcn_readlane(rseg[mb], min(last, 31)) : -1;
-    }
-    s_lo = blo[0];
-    s_hi = bhi[kDMB - 1] >= 0 ? bhi[kDMB - 1] : bhi[0];
-    la = s_lo + lane <= s_hi ? r.seg_adapter[s_lo + lane] : 0;
-    llive0 = la == 0 ? 0 : live_rank(L, la, jlo);
   }
 
   // LoRA second factor: the wave's share of the segments s_lo..s_hi crossing its rows
