@@ -29,6 +29,7 @@
 namespace {
 
 using namespace mlora;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));  // (the non-temporal builtins' operand type)
 
 constexpr int kDThreads = 512;
 constexpr int kDRows = 256;               // rows of the tile: every token of the pass
@@ -308,13 +309,15 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
   if (!RANGES && L.n_mats > 0 && mid != nullptr) lds_sync();
 
   if constexpr (RANGES) {
-    // this range's float32 tile, in the accumulators' order
+    // this range's float32 tile, in the accumulators' order (non-temporal stores: read once, by the expand launch,
+    // whose loads are non-temporal too; with plain stores and loads both launches took longer)
 #pragma unroll
     for (int mb = 0; mb < kDMB; ++mb)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        part[part_index(ks, n_tiles, nt, wave, mb, g, lane)] =
-            make_float4(acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]);
+        __builtin_nontemporal_store(
+            (f32x4_t){acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]},
+            reinterpret_cast<f32x4_t*>(&part[part_index(ks, n_tiles, nt, wave, mb, g, lane)]));
     return;
   }
 
@@ -583,7 +586,11 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
     for (int i = 0; i < 4; ++i)
       if (k0 + i < ksplit)
 #pragma unroll
-        for (int e = 0; e < kDMB * 4; ++e) u[i][e] = part[part_index(k0 + i, n_tiles, nt, wave, e / 4, e % 4, lane)];
+        for (int e = 0; e < kDMB * 4; ++e) {
+          const f32x4_t v = __builtin_nontemporal_load(
+              reinterpret_cast<const f32x4_t*>(&part[part_index(k0 + i, n_tiles, nt, wave, e / 4, e % 4, lane)]));
+          u[i][e] = make_float4(v.x, v.y, v.z, v.w);
+        }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (k0 + i < ksplit)
