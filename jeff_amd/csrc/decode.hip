@@ -368,7 +368,7 @@ __global__ __launch_bounds__(kDThreads) void dec_kernel(mlora_int4_t w, mlora_lo
             const int col = cw0 - oj + row;
             const int ccr = col >= 0 && col < cj ? col : 0;
             const uint32_t off = (uint32_t)((ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8)) * 2);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i4 * 8 * kTK), 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i4 * 8 * kTK), 16, off, 0, 0, kReadOnce);
           }
         };
         {
@@ -661,10 +661,10 @@ __global__ __launch_bounds__(kEThreads) void dec_expand_kernel(mlora_lora_t L, m
             const int ccr = col >= 0 && col < cj ? col : 0;
             const int q = ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8);
             if constexpr (GATED)
-              __builtin_amdgcn_global_load_lds((const void*)(blk + q), (lds_void*)(slot + i4 * 8 * kTK), 16, 0, 0);
+              __builtin_amdgcn_global_load_lds((const void*)(blk + q), (lds_void*)(slot + i4 * 8 * kTK), 16, 0, kReadOnce);
             else
               __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i4 * 8 * kTK), 16, (uint32_t)q * 2, 0,
-                                                       0, 0);
+                                                       0, kReadOnce);
           }
         };
         uint16_t* const slot0 = d_x2 + ew * 32 * kTK;  // (the base launch's x buffers: 4 KB a wave in each)

@@ -76,7 +76,7 @@ __device__ __forceinline__ void shrink_seg_block(const mlora_lora_t& L, const ml
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the buffer are done
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(buf + i * 8 * kDChunk), 16, aoff[i], kc * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(buf + i * 8 * kDChunk), 16, aoff[i], kc * 2, 0, kReadOnce);
   };
   const int chunks = k / kDChunk;
   const int ch0 = (wave * chunks) / kDWaves, ch1 = ((wave + 1) * chunks) / kDWaves;  // this wave's chunks
