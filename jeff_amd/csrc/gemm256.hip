@@ -282,7 +282,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         const int col = c0 + row;
         const int ccr = col >= 0 && col < cj ? col : 0;
         const uint32_t off = (uint32_t)((ccr * sbs + min(rc + 8 * swz_slot(row, lane & 7), sbs - 8)) * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i * 8 * kTK), 16, off, 0, 0, kReadOnce);
+        // (read once in decode-shaped passes, whose segments fit a row tile; a prefill segment's sB is re-read by
+        // each of its row tiles and stays cacheable)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(slot + i * 8 * kTK), 16, off, 0, 0,
+                                                 EARLY ? kReadOnce : 0);
       }
     };
     // the wave's operands of a staged segment (lane l: column l & 31, ranks 16 k16 + 8 (l >> 5) .. +7 of the chunk),
