@@ -31,6 +31,7 @@
 namespace {
 
 using namespace mlora;
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));  // (the non-temporal store's operand type)
 
 constexpr int kTM = 256, kTN = 256;
 constexpr int kThreads = 512;
@@ -50,7 +51,9 @@ __shared__ int32_t g_last[kTM];  // the tile's rows: request whose last token it
 // of tiles);
 // GATED: the gated epilogue (silu(gate) * up, inter columns), a template parameter so the plain kernel carries none of it;
 // EARLY: the kernel may add the LoRA term before the K loop (decode-shaped passes, below). The prefill kernels carry
-// no such path: with it, the compiler waits for every load in flight at the top of each round of the K loop.
+// no such path: with it, the compiler waits for every load in flight at the top of each round of the K loop. The
+// EARLY kernels also write their output tiles with non-temporal stores (decode-pool-28l's step 32.5 -> 31.6 ms: less
+// left to write back at each launch's end); a long prefill launch measured no better, or slightly worse, with them.
 template <int MB, bool GATED, bool EARLY>
 __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, mlora_lora_t L, mlora_route_t r,
                                                                const uint16_t* __restrict__ x, int64_t x_stride,
@@ -647,7 +650,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
       const uint4 v = silu_mul8(*reinterpret_cast<const uint4*>(&gb[off]), *reinterpret_cast<const uint4*>(&ub[off]));
       const int col = nt * 128 + c * 8;
       if (vec & kStoreVec) {
-        *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
+        if constexpr (EARLY)  // (decode-shaped: non-temporal)
+          __builtin_nontemporal_store((u32x4_t){v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(y + orig * y_stride + col));
+        else
+          *reinterpret_cast<uint4*>(y + orig * y_stride + col) = v;
         if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * inter + col) = v;
       } else {
         const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
@@ -676,7 +682,10 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
         const uint4 rv = *reinterpret_cast<const uint4*>(yr);
         v = make_uint4(add_bf16x2(rv.x, v.x), add_bf16x2(rv.y, v.y), add_bf16x2(rv.z, v.z), add_bf16x2(rv.w, v.w));
       }
-      *reinterpret_cast<uint4*>(yr) = v;
+      if constexpr (EARLY)  // (decode-shaped: non-temporal)
+        __builtin_nontemporal_store((u32x4_t){v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(yr));
+      else
+        *reinterpret_cast<uint4*>(yr) = v;
       if (lq >= 0) *reinterpret_cast<uint4*>(last_out + lq * n_out + col) = v;
     } else {
       const uint32_t e4[4] = {v.x, v.y, v.z, v.w};
@@ -697,17 +706,23 @@ __global__ __launch_bounds__(kThreads) void base_mfma256_kernel(mlora_int4_t w, 
 // its segments' sB rather than to its K loop) 128 rows when that is strictly fewer, e.g. 4096 decode rows through
 // 2048 columns: 128 tiles of 256 rows leave half the CUs idle. Split launches keep 256 (their range count is sized
 // for 256-row tiles).
-int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit, bool short_segs) {
-  if (ksplit != 1) return 8;
+// The current device's compute units (0 if unknown), read once per device.
+static int device_cus() {
   static int cus[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 8;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus[dev] = 0;
-  if (cus[dev] <= 0) return 8;
+  return cus[dev] > 0 ? cus[dev] : 0;
+}
+
+int tile_blocks(int64_t tokens, int n_tiles, int32_t ksplit, bool short_segs) {
+  if (ksplit != 1) return 8;
+  const int cus = device_cus();
+  if (cus <= 0) return 8;
   auto cost = [&](int mb) {
     const int64_t tiles = ((tokens + 32 * mb - 1) / (32 * mb)) * n_tiles;
-    return ((tiles + cus[dev] - 1) / cus[dev]) * mb;
+    return ((tiles + cus - 1) / cus) * mb;
   };
   const int best = cost(7) < cost(8) ? 7 : 8;
   return short_segs && cost(4) < cost(best) ? 4 : best;
